@@ -1,0 +1,125 @@
+/*
+ * narhip -- MI355X (gfx950) kernels for NAR's online rotate-and-quantize path.
+ *
+ * C ABI: plain pointers (device memory unless stated), sizes in elements,
+ * the HIP stream to launch on.  Every entry point validates its arguments on
+ * the host, launches asynchronously on `stream`, and returns NARHIP_OK or a
+ * negative code; narhip_last_error_string() then describes the failure (per
+ * calling thread).  No entry point allocates device memory: scratch space is
+ * passed in through `workspace` (size from the matching *_workspace query).
+ *
+ * Layouts (row-major, identical to the reference's):
+ *   x        bf16 [tokens, ld_x]                     (ld_x >= n, ld_x % 8 == 0)
+ *   v        fp32 [n, k]      Y'  (u = x V)
+ *   w_t      fp32 [k, n]      W''^T (x' = H x - u W''^T, i.e. U = -W'')
+ *   partial  fp32 [tokens, splits*k], partial[t, s*k + r] = sum over split s
+ *   codes    uint8 [rows, n/2], byte j = q[2j] | q[2j+1] << 4
+ *   scales, zeros  fp16 [rows, n/group]
+ * with rows = tokens, or the destination rows named by dest_rows[t].
+ */
+#ifndef NARHIP_H
+#define NARHIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NARHIP_ABI_VERSION 1
+
+enum {
+    NARHIP_OK = 0,
+    NARHIP_EINVAL = -1,        /* invalid argument (maps to ValueError)   */
+    NARHIP_EUNSUPPORTED = -2,  /* shape/mode not built (ValueError)       */
+    NARHIP_EHIP = -3,          /* HIP runtime error (RuntimeError)        */
+    NARHIP_EWORKSPACE = -4     /* workspace missing or too small          */
+};
+
+/* Rank-k arithmetic selection for narhip_rotate_quant / narhip_group_quant. */
+enum {
+    NARHIP_RANK_AUTO = 0,      /* MFMA for k >= 16 over a full row, else exact */
+    NARHIP_RANK_EXACT = 1,     /* fp64 accumulation, one rounding (VALU)       */
+    NARHIP_RANK_MFMA = 2       /* bf16 MFMA with split-precision factor terms  */
+};
+
+/* ABI version of the loaded library (NARHIP_ABI_VERSION at build time). */
+int narhip_abi_version(void);
+
+/* Message for the last failing call on this thread ("" if none). */
+const char *narhip_last_error_string(void);
+
+/* Host memory: the +-1 Paley Hadamard factor of order m (12 or 28) that the
+ * kernels use, row-major int8 [m, m].  Replaces the constructions
+ * _paley_hadamard_12 (nar/extended_experiment.py:459-472) and
+ * paley_hadamard_28 (nar/activation_experiments.py:114-128), unnormalised. */
+int narhip_paley(int32_t m, int8_t *out_host);
+
+/* Fused rotate -> rank-k -> INT4 quantize (one call per batch of tokens).
+ *
+ * Replaces, for one call: full_hadamard_rows(x, signs)
+ * (nar/activation_experiments.py:188-217) or the block FWHT of
+ * nar/kernels/r4_fused_v2.py:43-52, the rank-k term of
+ * quarot-llama3/nar_r4_kernel.py:190-202, and dynamic_asym_int4
+ * (nar/experiment.py:158-184) with the packed layout of
+ * nar/kernels/r4_fused_v2.py:67-92 -- i.e. the Python launchers
+ * launch_nar_fused / launch_hadamard (nar/kernels/r4_fused_v2.py:327-350).
+ *
+ *   had_m, had_q : Hadamard blocks of had_m*had_q channels get H_m (x) H_q;
+ *                  had_m in {1, 12, 28}, had_q a power of two in [128, 1024].
+ *                  had_m = 1 with had_q < n is the block Hadamard of nar/kernels.
+ *   signs        : fp32 [n] or NULL, applied to the Hadamard input only.
+ *   k            : rank (0 = Hadamard only), <= 64.
+ *   rank_block   : n (one projection over the row) or had_q (independent
+ *                  per-block factors, e.g. per KV head; needs k <= 8).
+ *   partial      : optional precomputed projection partials (splits >= 1);
+ *                  NULL = computed here.
+ *   group        : 32, 64 or 128, dividing had_q.
+ *   rotated      : optional fp32 [tokens, n] copy of x' before quantization.
+ *   dest_rows    : optional int64 [tokens]: token t writes output row dest_rows[t]
+ *                  (a KV-cache slot); NULL = row t.
+ *   rank_mode    : NARHIP_RANK_*.
+ */
+int narhip_rotate_quant(const void *x_bf16, int64_t tokens, int64_t n, int64_t ld_x,
+                        int32_t had_m, int32_t had_q, const float *signs,
+                        int32_t k, int64_t rank_block, const float *v, const float *w_t,
+                        const float *partial, int32_t splits,
+                        int32_t group, uint8_t *codes, void *scales_f16, void *zeros_f16,
+                        float *rotated, const int64_t *dest_rows, int32_t rank_mode,
+                        void *workspace, size_t workspace_bytes, void *stream);
+
+/* Workspace bytes narhip_rotate_quant needs for these arguments
+ * (0 when none; have_partial = 1 when the caller passes partials). */
+size_t narhip_rotate_quant_workspace(int64_t tokens, int64_t n, int32_t had_m, int32_t had_q,
+                                     int32_t k, int64_t rank_block, int32_t have_partial,
+                                     int32_t splits, int32_t rank_mode);
+
+/* Kernel A: rank-k projection partials.
+ * Replaces projection_triton_fp32 / rank_projection_kernel
+ * (nar/kernels/r4_fused_v2.py:122-152, 292-303) and launch_projection_dot
+ * (nar/kernels/r4_fused_v3.py:83-135, 187-201): partial[t, s*k + r] holds the
+ * sum over the s-th of `splits` equal channel chunks. */
+int narhip_rank_projection(const void *x_bf16, int64_t tokens, int64_t n, int64_t ld_x,
+                           const float *v, int32_t k, int32_t splits, float *partial,
+                           int32_t rank_mode, void *stream);
+
+/* Kernel B: rotate, fold the split partials into u, subtract u W''^T, quantize.
+ * Replaces nar_group_quant_kernel / launch_nar (nar/kernels/r4_fused_v2.py:
+ * 155-178, 306-324; nar/kernels/r4_fused_v3.py:206-234, 251-261). */
+int narhip_group_quant(const void *x_bf16, int64_t tokens, int64_t n, int64_t ld_x,
+                       int32_t had_m, int32_t had_q, const float *partial, int32_t splits,
+                       int32_t k, const float *w_t, int32_t group,
+                       uint8_t *codes, void *scales_f16, void *zeros_f16,
+                       void *workspace, size_t workspace_bytes, void *stream);
+
+/* Dequantize packed codes: out[r, i] = q * s + z (fp32 multiply then add).
+ * Replaces dequantize (nar/kernels/r4_fused_v2.py:364-369). */
+int narhip_dequantize(const uint8_t *codes, const void *scales_f16, const void *zeros_f16,
+                      int64_t rows, int64_t n, int32_t group, float *out, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NARHIP_H */

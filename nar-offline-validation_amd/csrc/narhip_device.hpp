@@ -1,0 +1,153 @@
+// Device-side building blocks shared by the NAR rotate-and-quantize kernels.
+//
+// gfx950 (CDNA4), wave64.  Every fp32 operation that the reference pins is
+// written so that it compiles to exactly one IEEE round-to-nearest-even
+// operation: butterflies are plain add/sub (or fma with a +-1 multiplier,
+// which is exact), divisions use the correctly rounded fp32 divide, rounding
+// to integers uses v_rndne.  The library is built without fast-math and
+// without fp32 denormal flushing.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+namespace narhip {
+
+// ------------------------------------------------------------ conversions --
+
+__device__ __forceinline__ float bf16lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// fp32 -> fp16 bits, round to nearest even (hardware v_cvt_f16_f32, default
+// rounding mode), subnormals and overflow to infinity as IEEE.
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float f)
+{
+    return __half_as_ushort(__float2half_rn(f));
+}
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t h)
+{
+    return __half2float(__ushort_as_half(h));
+}
+
+// ----------------------------------------------------- row-local exchange --
+//
+// A "row" is 16 consecutive lanes.  The kernels map the 4 lane bits of a row
+// to 4 bits of a segment position through
+//     chunk(L) = (l0^l2) | (l1^l2)<<1 | (l2^l3)<<2 | l3<<3
+// so that flipping chunk bit j is a lane exchange with xor mask 1, 2, 7, 15 --
+// exactly the DPP patterns quad_perm[1,0,3,2], quad_perm[2,3,0,1],
+// row_half_mirror and row_mirror.  Every butterfly stage that crosses lanes is
+// therefore one DPP move within the row, with no LDS traffic.
+
+enum : int {
+    DPP_XOR1 = 0xB1,         // quad_perm [1,0,3,2]
+    DPP_XOR2 = 0x4E,         // quad_perm [2,3,0,1]
+    DPP_XOR7 = 0x141,        // row_half_mirror
+    DPP_XOR15 = 0x140,       // row_mirror
+};
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v)
+{
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+template <int CTRL>
+__device__ __forceinline__ double dpp_f64(double v)
+{
+    int lo = __builtin_amdgcn_mov_dpp(__double2loint(v), CTRL, 0xF, 0xF, false);
+    int hi = __builtin_amdgcn_mov_dpp(__double2hiint(v), CTRL, 0xF, 0xF, false);
+    return __hiloint2double(hi, lo);
+}
+
+// Lane exchange for cross-lane butterfly stage j (0..3) within a row.
+template <int J>
+__device__ __forceinline__ float xchg(float v)
+{
+    if constexpr (J == 0) return dpp_f32<DPP_XOR1>(v);
+    else if constexpr (J == 1) return dpp_f32<DPP_XOR2>(v);
+    else if constexpr (J == 2) return dpp_f32<DPP_XOR7>(v);
+    else return dpp_f32<DPP_XOR15>(v);
+}
+
+template <int J>
+__device__ __forceinline__ double xchg64(double v)
+{
+    if constexpr (J == 0) return dpp_f64<DPP_XOR1>(v);
+    else if constexpr (J == 1) return dpp_f64<DPP_XOR2>(v);
+    else if constexpr (J == 2) return dpp_f64<DPP_XOR7>(v);
+    else return dpp_f64<DPP_XOR15>(v);
+}
+
+__device__ __forceinline__ int lane_chunk(int l16)
+{
+    int l0 = l16 & 1, l1 = (l16 >> 1) & 1, l2 = (l16 >> 2) & 1, l3 = (l16 >> 3) & 1;
+    return (l0 ^ l2) | ((l1 ^ l2) << 1) | ((l2 ^ l3) << 2) | (l3 << 3);
+}
+
+// Sum over the 16 lanes of a row in fp64; every lane receives the identical value.
+__device__ __forceinline__ double row_sum64(double v)
+{
+    v += xchg64<0>(v);
+    v += xchg64<1>(v);
+    v += xchg64<2>(v);
+    v += xchg64<3>(v);
+    return v;
+}
+
+// Min/max over the lanes of a group of G8 chunks (G8 = 4, 8 or 16 lanes, the
+// lanes whose chunk indices share chunk >> log2(G8)).  Exact in any order.
+template <int G8>
+__device__ __forceinline__ void group_minmax(float &lo, float &hi)
+{
+    lo = fminf(lo, xchg<0>(lo)); hi = fmaxf(hi, xchg<0>(hi));
+    lo = fminf(lo, xchg<1>(lo)); hi = fmaxf(hi, xchg<1>(hi));
+    if constexpr (G8 >= 8) { lo = fminf(lo, xchg<2>(lo)); hi = fmaxf(hi, xchg<2>(hi)); }
+    if constexpr (G8 >= 16) { lo = fminf(lo, xchg<3>(lo)); hi = fmaxf(hi, xchg<3>(hi)); }
+}
+
+// ------------------------------------------------------------- quantizer --
+//
+// dynamic_asym_int4 group parameters (nar/experiment.py:166-181):
+//   raw = (hi - lo) / 15 (fp32 division); s16 = fp16(raw > 0 ? raw : 1);
+//   s16 <= 0 -> 1; z16 = fp16(lo).
+struct GroupParams {
+    float s, z;
+    uint16_t s16, z16;
+};
+
+__device__ __forceinline__ GroupParams group_params(float lo, float hi)
+{
+    GroupParams g;
+    float raw = (hi - lo) / 15.0f;
+    float sr = raw > 0.0f ? raw : 1.0f;
+    uint16_t sh = f32_to_f16_bits(sr);
+    if (!(f16_bits_to_f32(sh) > 0.0f)) sh = 0x3c00u;
+    uint16_t zh = f32_to_f16_bits(lo);
+    g.s16 = sh; g.z16 = zh;
+    g.s = f16_bits_to_f32(sh);
+    g.z = f16_bits_to_f32(zh);
+    return g;
+}
+
+// q = clamp(round_half_even((x - z) / s), 0, 15) with the fp32 subtraction and
+// the correctly rounded fp32 division of the reference.
+__device__ __forceinline__ uint32_t quant_code(float x, const GroupParams &g)
+{
+    float d = x - g.z;
+    float q = __builtin_rintf(d / g.s);
+    q = fminf(fmaxf(q, 0.0f), 15.0f);
+    return (uint32_t)q;
+}
+
+// ----------------------------------------------------------------- Paley --
+
+// Rows of the +-1 Paley matrices as bit masks: bit a' of row a set <=> entry -1.
+// Filled from the construction of the reference (Paley I over Z_11 for 12,
+// over GF(27) for 28) by the host at library load.
+struct PaleyTable {
+    uint32_t neg[28];
+};
+
+}  // namespace narhip

@@ -1,0 +1,203 @@
+// Segment kernel: Hadamard blocks of Q <= 1024 channels, each handled by one
+// 16-lane row, fused with the rank-k term and the INT4 group quantizer.
+//
+// Covers the per-head paths (K/V cache: H_128 per head, per-head rank-k factors,
+// groups of 32) and the block-Hadamard paths of nar/kernels (block-H_128,
+// groups of 128, rank-k from a full-row projection given as split partials).
+//
+// Data layout in registers: segment position p = hi*128 + chunk(lane)*8 + e,
+// e in [0,8) the element inside one 16-byte bf16 load, hi in [0, Q/128).
+// Stages w = 1,2,4 are in-register, w = 8..64 are DPP exchanges inside the row,
+// w = 128.. are in-register again -- the reference's stage order
+// (nar/extended_experiment.py:443-456) is preserved exactly.
+#include "narhip_device.hpp"
+
+namespace narhip {
+
+enum RankMode : int { RANK_NONE = 0, RANK_LOCAL = 1, RANK_PARTIAL = 2 };
+
+struct SegArgs {
+    const uint16_t *x;      // bf16 [T, ldx]
+    int64_t ldx;
+    int64_t T, n;           // tokens, channels per token
+    const float *signs;     // [n] or null
+    const float *v;         // [n, k] (RANK_LOCAL)
+    const float *wt;        // [k, n]
+    const float *partial;   // [T, splits*k] (RANK_PARTIAL)
+    int splits;
+    int k;
+    uint8_t *codes;         // [rows_out, n/2]
+    uint16_t *scales;       // [rows_out, n/B]
+    uint16_t *zeros;
+    const int64_t *dest;    // [T] output row per token, or null
+    float *rotated;         // [T, n] or null
+    float sq;               // fp32(sqrt(Q)), computed on the host
+};
+
+template <int Q, int B, int MODE, int KMAX>
+__global__ void __launch_bounds__(256)
+rq_seg_kernel(SegArgs a)
+{
+    constexpr int NH = Q / 128;          // 128-position chunks per segment
+    constexpr int NV = 8 * NH;           // values per lane
+    constexpr int G8 = B / 8;            // lanes per quant group (4, 8, 16)
+    const int lane = threadIdx.x & 63;
+    const int l16 = lane & 15;
+    const int row = threadIdx.x >> 4;    // 16 rows per block
+    const int64_t segs_per_token = a.n / Q;
+    const int64_t seg = (int64_t)blockIdx.x * 16 + row;
+    const bool active = seg < a.T * segs_per_token;
+    const int64_t sg = active ? seg : 0;
+    const int64_t t = sg / segs_per_token;
+    const int64_t base = (sg % segs_per_token) * Q;   // channel offset in the token
+    const int chunk = lane_chunk(l16);
+
+    // ---- load: NH x 16-byte bf16 loads per lane
+    float v[NV];
+    uint32_t raw[NV / 2];
+    const uint16_t *xr = a.x + t * a.ldx + base;
+#pragma unroll
+    for (int h = 0; h < NH; h++) {
+        uint4 w = *reinterpret_cast<const uint4 *>(xr + h * 128 + chunk * 8);
+        raw[h * 4 + 0] = w.x; raw[h * 4 + 1] = w.y; raw[h * 4 + 2] = w.z; raw[h * 4 + 3] = w.w;
+    }
+#pragma unroll
+    for (int i = 0; i < NV / 2; i++) {
+        v[2 * i] = bf16lo(raw[i]);
+        v[2 * i + 1] = bf16hi(raw[i]);
+    }
+
+    // ---- rank-k projection of the raw input (fp64, rounded once to fp32)
+    float u[KMAX > 0 ? KMAX : 1];
+    if constexpr (MODE == RANK_LOCAL) {
+        double acc[KMAX];
+#pragma unroll
+        for (int r = 0; r < KMAX; r++) acc[r] = 0.0;
+#pragma unroll
+        for (int h = 0; h < NH; h++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const int64_t ch = base + h * 128 + chunk * 8 + e;
+                const double xv = (double)v[h * 8 + e];
+#pragma unroll
+                for (int r = 0; r < KMAX; r++)
+                    if (r < a.k) acc[r] = fma(xv, (double)a.v[ch * a.k + r], acc[r]);
+            }
+#pragma unroll
+        for (int r = 0; r < KMAX; r++) u[r] = (float)row_sum64(acc[r]);
+    } else if constexpr (MODE == RANK_PARTIAL) {
+        const float *p = a.partial + t * (int64_t)a.splits * a.k;
+#pragma unroll
+        for (int r = 0; r < KMAX; r++) {
+            double s = 0.0;
+            if (r < a.k)
+                for (int sp = 0; sp < a.splits; sp++) s += (double)p[sp * a.k + r];
+            u[r] = (float)s;
+        }
+    }
+
+    // ---- signs (Hadamard input only)
+    if (a.signs) {
+#pragma unroll
+        for (int h = 0; h < NH; h++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) v[h * 8 + e] *= a.signs[base + h * 128 + chunk * 8 + e];
+    }
+
+    // ---- FWHT_Q, stages w = 1, 2, 4 (in-register)
+#pragma unroll
+    for (int w = 1; w < 8; w <<= 1)
+#pragma unroll
+        for (int h = 0; h < NH; h++)
+#pragma unroll
+            for (int e = 0; e < 8; e++)
+                if (!(e & w)) {
+                    float x0 = v[h * 8 + e], x1 = v[h * 8 + e + w];
+                    v[h * 8 + e] = x0 + x1;
+                    v[h * 8 + e + w] = x0 - x1;
+                }
+    // stages w = 8, 16, 32, 64 (DPP inside the row): lower lane x+p, upper p-x
+    {
+        const float s0 = (chunk & 1) ? -1.0f : 1.0f;
+        const float s1 = (chunk & 2) ? -1.0f : 1.0f;
+        const float s2 = (chunk & 4) ? -1.0f : 1.0f;
+        const float s3 = (chunk & 8) ? -1.0f : 1.0f;
+#pragma unroll
+        for (int i = 0; i < NV; i++) v[i] = __builtin_fmaf(s0, v[i], xchg<0>(v[i]));
+#pragma unroll
+        for (int i = 0; i < NV; i++) v[i] = __builtin_fmaf(s1, v[i], xchg<1>(v[i]));
+#pragma unroll
+        for (int i = 0; i < NV; i++) v[i] = __builtin_fmaf(s2, v[i], xchg<2>(v[i]));
+#pragma unroll
+        for (int i = 0; i < NV; i++) v[i] = __builtin_fmaf(s3, v[i], xchg<3>(v[i]));
+    }
+    // stages w = 128, 256, ... (in-register across hi)
+#pragma unroll
+    for (int wh = 1; wh < NH; wh <<= 1)
+#pragma unroll
+        for (int h = 0; h < NH; h++)
+            if (!(h & wh))
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    float x0 = v[h * 8 + e], x1 = v[(h + wh) * 8 + e];
+                    v[h * 8 + e] = x0 + x1;
+                    v[(h + wh) * 8 + e] = x0 - x1;
+                }
+    // normalisation: fp32 division by fp32(sqrt(Q))
+    {
+        const float sq = a.sq;
+#pragma unroll
+        for (int i = 0; i < NV; i++) v[i] = v[i] / sq;
+    }
+
+    // ---- rank-k correction: x' = Hx - RN32(sum_r u_r W[r, i])
+    if constexpr (MODE != RANK_NONE) {
+#pragma unroll
+        for (int h = 0; h < NH; h++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const int64_t ch = base + h * 128 + chunk * 8 + e;
+                double acc = 0.0;
+#pragma unroll
+                for (int r = 0; r < KMAX; r++)
+                    if (r < a.k) acc = fma((double)u[r], (double)a.wt[(int64_t)r * a.n + ch], acc);
+                v[h * 8 + e] = v[h * 8 + e] - (float)acc;
+            }
+    }
+
+    if (a.rotated && active) {
+        float *o = a.rotated + t * a.n + base;
+#pragma unroll
+        for (int h = 0; h < NH; h++) {
+            float4 *d = reinterpret_cast<float4 *>(o + h * 128 + chunk * 8);
+            d[0] = make_float4(v[h * 8 + 0], v[h * 8 + 1], v[h * 8 + 2], v[h * 8 + 3]);
+            d[1] = make_float4(v[h * 8 + 4], v[h * 8 + 5], v[h * 8 + 6], v[h * 8 + 7]);
+        }
+    }
+
+    // ---- quantize groups of B and store
+    const int64_t orow = a.dest ? a.dest[t] : t;
+    const int64_t gpt = a.n / B;   // groups per token
+#pragma unroll
+    for (int h = 0; h < NH; h++) {
+        float lo = v[h * 8], hi = v[h * 8];
+#pragma unroll
+        for (int e = 1; e < 8; e++) { lo = fminf(lo, v[h * 8 + e]); hi = fmaxf(hi, v[h * 8 + e]); }
+        group_minmax<G8>(lo, hi);
+        const GroupParams g = group_params(lo, hi);
+        uint32_t word = 0;
+#pragma unroll
+        for (int e = 0; e < 8; e++) word |= quant_code(v[h * 8 + e], g) << (4 * e);
+        if (active) {
+            const int64_t pos = base + h * 128 + chunk * 8;
+            *reinterpret_cast<uint32_t *>(a.codes + orow * (a.n / 2) + pos / 2) = word;
+            if ((chunk & (G8 - 1)) == 0) {
+                const int64_t gi = orow * gpt + pos / B;
+                a.scales[gi] = g.s16;
+                a.zeros[gi] = g.z16;
+            }
+        }
+    }
+}
+
+}  // namespace narhip

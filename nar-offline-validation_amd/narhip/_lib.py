@@ -1,0 +1,70 @@
+"""ctypes binding of libnarhip.so (include/narhip.h).
+
+The library is built in-tree by narhip/build.py.  Loading fails loudly when it
+is missing: there is no CPU or PyTorch fallback for any operator.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libnarhip.so"
+
+NARHIP_OK = 0
+NARHIP_EINVAL = -1
+NARHIP_EUNSUPPORTED = -2
+NARHIP_EHIP = -3
+NARHIP_EWORKSPACE = -4
+
+RANK_AUTO = 0
+RANK_EXACT = 1
+RANK_MFMA = 2
+
+EXPORTS = (
+    "narhip_abi_version", "narhip_last_error_string", "narhip_paley",
+    "narhip_rotate_quant", "narhip_rotate_quant_workspace",
+    "narhip_rank_projection", "narhip_group_quant", "narhip_dequantize",
+)
+
+_lib: ctypes.CDLL | None = None
+
+c_i32, c_i64, c_sz, c_p = ctypes.c_int32, ctypes.c_int64, ctypes.c_size_t, ctypes.c_void_p
+
+
+def load() -> ctypes.CDLL:
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise ImportError(f"{LIB_PATH} is not built; run narhip/build.py (or __graft_entry__.build())")
+    lib = ctypes.CDLL(str(LIB_PATH))
+    lib.narhip_abi_version.restype = ctypes.c_int
+    lib.narhip_last_error_string.restype = ctypes.c_char_p
+    lib.narhip_paley.argtypes = [c_i32, c_p]
+    lib.narhip_rotate_quant.argtypes = [
+        c_p, c_i64, c_i64, c_i64, c_i32, c_i32, c_p,
+        c_i32, c_i64, c_p, c_p, c_p, c_i32,
+        c_i32, c_p, c_p, c_p, c_p, c_p, c_i32, c_p, c_sz, c_p]
+    lib.narhip_rotate_quant_workspace.argtypes = [c_i64, c_i64, c_i32, c_i32, c_i32, c_i64, c_i32, c_i32, c_i32]
+    lib.narhip_rotate_quant_workspace.restype = c_sz
+    lib.narhip_rank_projection.argtypes = [c_p, c_i64, c_i64, c_i64, c_p, c_i32, c_i32, c_p, c_i32, c_p]
+    lib.narhip_group_quant.argtypes = [
+        c_p, c_i64, c_i64, c_i64, c_i32, c_i32, c_p, c_i32, c_i32, c_p, c_i32,
+        c_p, c_p, c_p, c_p, c_sz, c_p]
+    lib.narhip_dequantize.argtypes = [c_p, c_p, c_p, c_i64, c_i64, c_i32, c_p, c_p]
+    for name in ("narhip_paley", "narhip_rotate_quant", "narhip_rank_projection",
+                 "narhip_group_quant", "narhip_dequantize"):
+        getattr(lib, name).restype = ctypes.c_int
+    _lib = lib
+    return lib
+
+
+def check(rc: int) -> None:
+    """Map a negative return code to the reference's exception types."""
+    if rc == NARHIP_OK:
+        return
+    msg = load().narhip_last_error_string().decode(errors="replace")
+    if rc in (NARHIP_EINVAL, NARHIP_EUNSUPPORTED, NARHIP_EWORKSPACE):
+        raise ValueError(msg)
+    raise RuntimeError(msg)

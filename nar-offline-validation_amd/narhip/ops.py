@@ -1,0 +1,185 @@
+"""Torch-facing wrappers of the narhip C ABI.
+
+Tensors stay on the GPU and are passed to the library as raw pointers; kernels
+run on the current HIP stream of the tensor's device.  Outputs are allocated
+here when the caller does not pass them (the reference's launchers take them
+preallocated; both forms are supported).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+
+import torch
+
+from . import _lib
+
+RANK_AUTO, RANK_EXACT, RANK_MFMA = _lib.RANK_AUTO, _lib.RANK_EXACT, _lib.RANK_MFMA
+
+
+def _p(t: torch.Tensor | None) -> ctypes.c_void_p | None:
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(device: torch.device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _require(t: torch.Tensor, dtype: torch.dtype, name: str, device: torch.device) -> None:
+    if t.dtype != dtype:
+        raise ValueError(f"{name} must be {dtype}, got {t.dtype}")
+    if t.device != device:
+        raise ValueError(f"{name} must be on {device}, got {t.device}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+def hadamard_factors(n: int) -> tuple[int, int]:
+    """(m, q) with n = m*q in the dispatch order of full_hadamard_rows
+    (nar/activation_experiments.py:190-201): 28 * 2^j first, then 12 * 2^j,
+    then a power of two."""
+    for m in (28, 12):
+        q, r = divmod(n, m)
+        if not r and q >= 1 and not q & (q - 1):
+            return m, q
+    if n > 0 and not n & (n - 1):
+        return 1, n
+    raise ValueError(f"no frozen full-Hadamard construction for n={n}")
+
+
+def paley(m: int) -> torch.Tensor:
+    """The +-1 Paley factor the kernels use (int8 [m, m], host)."""
+    out = torch.empty((m, m), dtype=torch.int8)
+    _lib.check(_lib.load().narhip_paley(m, _p(out)))
+    return out
+
+
+def rotate_quant(x: torch.Tensor, *, hadamard: tuple[int, int] = (1, 128),
+                 signs: torch.Tensor | None = None,
+                 v: torch.Tensor | None = None, w_t: torch.Tensor | None = None,
+                 rank_block: int | None = None,
+                 partial: torch.Tensor | None = None,
+                 group: int = 128,
+                 codes: torch.Tensor | None = None, scales: torch.Tensor | None = None,
+                 zeros: torch.Tensor | None = None,
+                 rotated: torch.Tensor | None = None,
+                 dest_rows: torch.Tensor | None = None,
+                 rank_mode: int = RANK_AUTO,
+                 out_rows: int | None = None):
+    """x' = H_s x - (x V) W^T, then dynamic asymmetric INT4 over groups of `group`.
+
+    x: bf16 [T, n] (row stride a multiple of 8).  v: fp32 [n, k], w_t: fp32 [k, n].
+    Returns (codes uint8 [R, n/2], scales fp16 [R, n/group], zeros fp16 [R, n/group]).
+    """
+    if x.dim() != 2:
+        raise ValueError("x must be 2-D [tokens, n]")
+    if x.dtype != torch.bfloat16:
+        raise ValueError(f"x must be bfloat16, got {x.dtype}")
+    if not x.is_cuda:
+        raise ValueError("x must be a GPU tensor")
+    if x.stride(1) != 1:
+        raise ValueError("x rows must be contiguous")
+    dev = x.device
+    T, n = x.shape
+    m, q = hadamard
+    k = 0 if w_t is None else int(w_t.shape[0])
+    if k:
+        _require(w_t, torch.float32, "w_t", dev)
+        if v is not None:
+            _require(v, torch.float32, "v", dev)
+            if v.shape != (n, k):
+                raise ValueError(f"v must be [{n}, {k}], got {tuple(v.shape)}")
+        if w_t.shape != (k, n):
+            raise ValueError(f"w_t must be [{k}, {n}], got {tuple(w_t.shape)}")
+    if signs is not None:
+        _require(signs, torch.float32, "signs", dev)
+    splits = 0
+    if partial is not None:
+        _require(partial, torch.float32, "partial", dev)
+        if not k or partial.shape[0] != T or partial.shape[1] % k:
+            raise ValueError("partial must be [tokens, splits*k]")
+        splits = partial.shape[1] // k
+    rows = T if out_rows is None else out_rows
+    if codes is None:
+        codes = torch.empty((rows, n // 2), dtype=torch.uint8, device=dev)
+    if scales is None:
+        scales = torch.empty((rows, n // group), dtype=torch.float16, device=dev)
+    if zeros is None:
+        zeros = torch.empty((rows, n // group), dtype=torch.float16, device=dev)
+    for t, name, dt in ((codes, "codes", torch.uint8), (scales, "scales", torch.float16),
+                        (zeros, "zeros", torch.float16)):
+        _require(t, dt, name, dev)
+    if rotated is not None:
+        _require(rotated, torch.float32, "rotated", dev)
+    if dest_rows is not None:
+        _require(dest_rows, torch.int64, "dest_rows", dev)
+    nb = n if rank_block is None else int(rank_block)
+    lib = _lib.load()
+    ws_bytes = lib.narhip_rotate_quant_workspace(T, n, m, q, k, nb, int(partial is not None), splits, rank_mode)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
+    rc = lib.narhip_rotate_quant(
+        _p(x), T, n, x.stride(0), m, q, _p(signs), k, nb, _p(v), _p(w_t), _p(partial), splits,
+        group, _p(codes), _p(scales), _p(zeros), _p(rotated), _p(dest_rows), rank_mode,
+        _p(ws), ws_bytes, _stream(dev))
+    _lib.check(rc)
+    return codes, scales, zeros
+
+
+def rank_projection(x: torch.Tensor, v: torch.Tensor, partial: torch.Tensor,
+                    rank_mode: int = RANK_AUTO) -> torch.Tensor:
+    """partial[t, s*k + r] = sum over channel split s of x[t, i] v[i, r]."""
+    if x.dtype != torch.bfloat16 or x.stride(1) != 1:
+        raise ValueError("x must be bfloat16 with contiguous rows")
+    dev = x.device
+    _require(v, torch.float32, "v", dev)
+    _require(partial, torch.float32, "partial", dev)
+    T, n = x.shape
+    k = int(v.shape[1])
+    if partial.shape[0] != T or partial.shape[1] % k:
+        raise ValueError("partial must be [tokens, splits*k]")
+    splits = partial.shape[1] // k
+    rc = _lib.load().narhip_rank_projection(_p(x), T, n, x.stride(0), _p(v), k, splits, _p(partial),
+                                            rank_mode, _stream(dev))
+    _lib.check(rc)
+    return partial
+
+
+def group_quant(x: torch.Tensor, partial: torch.Tensor | None, w_t: torch.Tensor | None,
+                codes: torch.Tensor, scales: torch.Tensor, zeros: torch.Tensor, *,
+                hadamard: tuple[int, int] = (1, 128), group: int = 128) -> None:
+    """Kernel B: rotate, fold the split partials, subtract u W^T, quantize."""
+    if x.dtype != torch.bfloat16 or x.stride(1) != 1:
+        raise ValueError("x must be bfloat16 with contiguous rows")
+    dev = x.device
+    T, n = x.shape
+    k = 0 if w_t is None else int(w_t.shape[0])
+    splits = 0
+    if k:
+        _require(w_t, torch.float32, "w_t", dev)
+        _require(partial, torch.float32, "partial", dev)
+        splits = partial.shape[1] // k
+    m, q = hadamard
+    lib = _lib.load()
+    ws_bytes = lib.narhip_rotate_quant_workspace(T, n, m, q, k, n, 1, splits, RANK_EXACT)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
+    rc = lib.narhip_group_quant(_p(x), T, n, x.stride(0), m, q, _p(partial), splits, k, _p(w_t), group,
+                                _p(codes), _p(scales), _p(zeros), _p(ws), ws_bytes, _stream(dev))
+    _lib.check(rc)
+
+
+def dequantize(codes: torch.Tensor, scales: torch.Tensor, zeros: torch.Tensor, n: int,
+               group: int) -> torch.Tensor:
+    dev = codes.device
+    _require(codes, torch.uint8, "codes", dev)
+    _require(scales, torch.float16, "scales", dev)
+    _require(zeros, torch.float16, "zeros", dev)
+    rows = codes.shape[0]
+    out = torch.empty((rows, n), dtype=torch.float32, device=dev)
+    _lib.check(_lib.load().narhip_dequantize(_p(codes), _p(scales), _p(zeros), rows, n, group,
+                                             _p(out), _stream(dev)))
+    return out
+
+
+def sqrt_f32(v: int) -> float:
+    return float(torch.tensor(math.sqrt(v), dtype=torch.float32))

