@@ -1,0 +1,205 @@
+#!/usr/bin/env python3
+"""Throughput of the fused NAR rotate -> rank-k -> INT4 path on one MI355X.
+
+One step = one call of the fused operator over one batch of synthetic tokens
+(default: the Llama-3.1-8B down_proj shape, 8192 x 14336 bf16, H_28 (x) H_512,
+k=32, b=128).  Inputs are resident in HBM before the timed region; R input and
+output buffers are rotated so that consecutive steps never reuse a buffer the
+256 MB Infinity Cache could still hold.
+
+Prints ONE JSON line (rank 0): tokens/s, achieved HBM GB/s from the algorithmic
+byte model T*(2n + n/2 + 4n/b) + factor bytes, the roofline of the dominant
+kernel (HIP-event timed on the stream it runs on) and the CPU baseline (the
+reference's PyTorch op sequence on a bounded sample of the same rows).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (str(ROOT), str(ROOT / "nar-offline-validation_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "fused NAR+INT4 quant: tokens/s and achieved HBM GB/s (% peak), 1 MI355X"
+HBM_PEAK_GBPS = 8000.0
+MALL_BYTES = 256 << 20
+
+
+def parse() -> argparse.Namespace:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="downproj_8b",
+                    choices=["kcache_3b", "qproj_3b", "downproj_8b", "vcache_decode_8b", "downproj_70b"])
+    ap.add_argument("--rank-mode", default="auto", choices=["auto", "exact", "mfma"])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU baseline work")
+    return ap.parse_args()
+
+
+def describe(w) -> str:
+    m, q = w.hadamard
+    had = f"H{q} per block" if m == 1 else f"H{m}xH{q}"
+    rb = "" if w.rank_block in (None, w.n) else f" per {w.rank_block}-block"
+    return f"{w.name}: {w.tokens} tokens x {w.n} bf16, {had}, k={w.k}{rb}, b={w.group}"
+
+
+def cpu_baseline(w, target_s: float) -> dict:
+    import torch
+
+    from oracle import torch_path
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    rows = min(w.tokens, 16)
+
+    def once(r: int) -> float:
+        t0 = time.perf_counter()
+        for lo in range(0, r, 1024):
+            hi = min(r, lo + 1024)
+            torch_path.run(w.x[lo:hi], *w.hadamard, w.v, w.w_t, w.group, w.rank_block)
+        return time.perf_counter() - t0
+
+    once(rows)
+    dt = once(rows)
+    while dt * 6 < target_s and rows < w.tokens:
+        rows = min(w.tokens, rows * 2)
+        dt = once(rows)
+    times = [once(rows) for _ in range(5)]
+    med = statistics.median(times)
+    model = ""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": rows / med, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"first {rows} of {w.tokens} rows of the same workload, torch CPU op sequence of the "
+                      f"reference (oracle/torch_path.py), median of 5 after 1 warmup; cpu: {model}"}
+
+
+def main() -> int:
+    args = parse()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: every box here has a single MI355X and the path "
+              "shards by tokens with no communication (see DESIGN.md); run with --gpus 1.",
+              file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+
+    from narhip import ops, workloads
+
+    mode = {"auto": ops.RANK_AUTO, "exact": ops.RANK_EXACT, "mfma": ops.RANK_MFMA}[args.rank_mode]
+    w = workloads.CONFIGS[args.config]()
+    dev = torch.device("cuda:0")
+    x_host = torch.from_numpy(w.x.view(np.int16))
+    in_bytes = w.x.nbytes
+    R = max(2, min(8, -(-2 * MALL_BYTES // max(in_bytes, 1)) + 1))
+    xs = [x_host.to(dev).view(torch.bfloat16) for _ in range(R)]
+    v = None if w.v is None else torch.from_numpy(w.v).to(dev)
+    wt = None if w.w_t is None else torch.from_numpy(w.w_t).to(dev)
+    rows_out = w.out_rows or w.tokens
+    outs = [(torch.empty((rows_out, w.n // 2), dtype=torch.uint8, device=dev),
+             torch.empty((rows_out, w.n // w.group), dtype=torch.float16, device=dev),
+             torch.empty((rows_out, w.n // w.group), dtype=torch.float16, device=dev)) for _ in range(R)]
+    dest = None if w.dest_rows is None else torch.from_numpy(w.dest_rows).to(dev)
+    full_row_rank = w.k > 0 and w.rank_block in (None, w.n)
+
+    def step(i: int) -> None:
+        c, s, z = outs[i % R]
+        ops.rotate_quant(xs[i % R], hadamard=w.hadamard, v=v, w_t=wt, rank_block=w.rank_block,
+                         group=w.group, codes=c, scales=s, zeros=z, dest_rows=dest, rank_mode=mode)
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize(dev)
+    stream = torch.cuda.current_stream(dev)
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record(stream)
+    for i in range(args.steps):
+        step(i)
+    ev1.record(stream)
+    torch.cuda.synchronize(dev)
+    wall = time.perf_counter() - t0
+    ms_total = ev0.elapsed_time(ev1)
+    ms_step = ms_total / args.steps
+
+    # Dominant kernel: stage B (rotate + correction + quantize).  For a full-row
+    # rank the projection (stage A) is launched separately so that B can be
+    # timed on its own with events on the same stream.
+    stage = {}
+    if full_row_rank:
+        splits = 1
+        partial = torch.empty((w.tokens, splits * w.k), dtype=torch.float32, device=dev)
+        ea = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        ta, tb = [], []
+        for i in range(args.warmup + args.steps):
+            c, s, z = outs[i % R]
+            ea[0].record(stream)
+            ops.rank_projection(xs[i % R], v, partial, rank_mode=mode)
+            ea[1].record(stream)
+            ops.rotate_quant(xs[i % R], hadamard=w.hadamard, v=v, w_t=wt, partial=partial, group=w.group,
+                             codes=c, scales=s, zeros=z, rank_mode=mode)
+            ea[2].record(stream)
+            torch.cuda.synchronize(dev)
+            if i >= args.warmup:
+                ta.append(ea[0].elapsed_time(ea[1]))
+                tb.append(ea[1].elapsed_time(ea[2]))
+        stage = {"projection_ms": statistics.mean(ta), "transform_quant_ms": statistics.mean(tb)}
+        dom_ms = stage["transform_quant_ms"]
+        dom_name = "transform_quant (FWHT, Paley, rank-k correction, INT4)"
+        factor_b = w.w_t.nbytes
+    else:
+        dom_ms = ms_step
+        dom_name = "rotate_quant (single fused kernel)"
+        factor_b = 0 if w.v is None else w.v.nbytes + w.w_t.nbytes
+
+    t, n, b = w.tokens, w.n, w.group
+    alg_bytes = w.algorithmic_bytes()
+    dom_bytes = t * (2 * n + n // 2 + 4 * n // b) + factor_b
+    achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
+    line = {
+        "metric": METRIC,
+        "value": t / (ms_step * 1e-3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded, narhip/workloads.py)",
+        "config": {"workload": describe(w), "tokens": t, "n": n, "hadamard": list(w.hadamard), "k": w.k,
+                   "group": b, "rank_mode": args.rank_mode, "rotated_buffers": R},
+        "achieved_gbps": alg_bytes / (ms_step * 1e-3) / 1e9,
+        "hbm_frac": alg_bytes / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBPS,
+        "wall_s": wall,
+        "stages_ms": stage,
+        "roofline": {"kernel": dom_name, "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": achieved / HBM_PEAK_GBPS, "traffic": None},
+    }
+    if w.dest_rows is not None:
+        line["us_per_call"] = ms_step * 1e3
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
