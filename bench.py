@@ -116,10 +116,12 @@ def main() -> int:
              torch.empty((rows_out, w.n // w.group), dtype=torch.float16, device=dev)) for _ in range(R)]
     dest = None if w.dest_rows is None else torch.from_numpy(w.dest_rows).to(dev)
     full_row_rank = w.k > 0 and w.rank_block in (None, w.n)
+    # factor terms are prepared once per factor set, as the reference's modules do
+    prepared = ops.prepare_rank_factors(v, wt, w.n, w.k) if full_row_rank and mode != ops.RANK_EXACT else None
 
     def step(i: int) -> None:
         c, s, z = outs[i % R]
-        ops.rotate_quant(xs[i % R], hadamard=w.hadamard, v=v, w_t=wt, rank_block=w.rank_block,
+        ops.rotate_quant(xs[i % R], hadamard=w.hadamard, v=v, w_t=wt, prepared=prepared, rank_block=w.rank_block,
                          group=w.group, codes=c, scales=s, zeros=z, dest_rows=dest, rank_mode=mode)
 
     for i in range(args.warmup):
@@ -142,17 +144,17 @@ def main() -> int:
     # timed on its own with events on the same stream.
     stage = {}
     if full_row_rank:
-        splits = 1
+        splits = 8 if prepared is not None else 1
         partial = torch.empty((w.tokens, splits * w.k), dtype=torch.float32, device=dev)
         ea = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
         ta, tb = [], []
         for i in range(args.warmup + args.steps):
             c, s, z = outs[i % R]
             ea[0].record(stream)
-            ops.rank_projection(xs[i % R], v, partial, rank_mode=mode)
+            ops.rank_projection(xs[i % R], v, partial, rank_mode=mode, prepared=prepared)
             ea[1].record(stream)
-            ops.rotate_quant(xs[i % R], hadamard=w.hadamard, v=v, w_t=wt, partial=partial, group=w.group,
-                             codes=c, scales=s, zeros=z, rank_mode=mode)
+            ops.rotate_quant(xs[i % R], hadamard=w.hadamard, v=v, w_t=wt, prepared=prepared, partial=partial,
+                             group=w.group, codes=c, scales=s, zeros=z, rank_mode=mode)
             ea[2].record(stream)
             torch.cuda.synchronize(dev)
             if i >= args.warmup:

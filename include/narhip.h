@@ -68,55 +68,77 @@ int narhip_paley(int32_t m, int8_t *out_host);
  *
  *   had_m, had_q : Hadamard blocks of had_m*had_q channels get H_m (x) H_q;
  *                  had_m in {1, 12, 28}, had_q a power of two in [128, 1024].
- *                  had_m = 1 with had_q < n is the block Hadamard of nar/kernels.
+ *                  had_m = 1 with had_q < n is the block Hadamard of nar/kernels;
+ *                  had_m > 1 requires had_m*had_q = n (one Kronecker row).
  *   signs        : fp32 [n] or NULL, applied to the Hadamard input only.
  *   k            : rank (0 = Hadamard only), <= 64.
  *   rank_block   : n (one projection over the row) or had_q (independent
  *                  per-block factors, e.g. per KV head; needs k <= 8).
+ *   v, w_t       : fp32 factors (see layouts above).
+ *   prepared     : optional output of narhip_prepare_rank_factors for (v, w_t);
+ *                  NULL = prepared in the workspace on every call.
  *   partial      : optional precomputed projection partials (splits >= 1);
  *                  NULL = computed here.
  *   group        : 32, 64 or 128, dividing had_q.
  *   rotated      : optional fp32 [tokens, n] copy of x' before quantization.
  *   dest_rows    : optional int64 [tokens]: token t writes output row dest_rows[t]
- *                  (a KV-cache slot); NULL = row t.
+ *                  (a KV-cache slot); NULL = row t.  Values must be valid rows.
  *   rank_mode    : NARHIP_RANK_*.
  */
 int narhip_rotate_quant(const void *x_bf16, int64_t tokens, int64_t n, int64_t ld_x,
                         int32_t had_m, int32_t had_q, const float *signs,
                         int32_t k, int64_t rank_block, const float *v, const float *w_t,
-                        const float *partial, int32_t splits,
+                        const void *prepared, const float *partial, int32_t splits,
                         int32_t group, uint8_t *codes, void *scales_f16, void *zeros_f16,
                         float *rotated, const int64_t *dest_rows, int32_t rank_mode,
                         void *workspace, size_t workspace_bytes, void *stream);
 
-/* Workspace bytes narhip_rotate_quant needs for these arguments
- * (0 when none; have_partial = 1 when the caller passes partials). */
+/* Workspace bytes narhip_rotate_quant needs for these arguments (0 when none;
+ * have_partial / have_prepared = 1 when the caller passes them). */
 size_t narhip_rotate_quant_workspace(int64_t tokens, int64_t n, int32_t had_m, int32_t had_q,
                                      int32_t k, int64_t rank_block, int32_t have_partial,
-                                     int32_t splits, int32_t rank_mode);
+                                     int32_t splits, int32_t have_prepared, int32_t rank_mode);
+
+/* Bytes of the prepared rank factors for (n, k): V and W''^T as three exact
+ * bf16 terms each in the MFMA layouts.  Replaces the term preparation of
+ * FoldedR4.from_factor (nar/fold_signed_permutation.py:80-95) and fp16_terms /
+ * w_terms (quarot-llama3/nar_r4_kernel.py:151-187). */
+size_t narhip_rank_factors_bytes(int64_t n, int32_t k);
+
+/* Fill `prepared` from fp32 v [n, k] and/or w_t [k, n] (either may be NULL to
+ * refresh only the other half). */
+int narhip_prepare_rank_factors(const float *v, const float *w_t, int64_t n, int32_t k,
+                                void *prepared, size_t prepared_bytes, void *stream);
 
 /* Kernel A: rank-k projection partials.
  * Replaces projection_triton_fp32 / rank_projection_kernel
  * (nar/kernels/r4_fused_v2.py:122-152, 292-303) and launch_projection_dot
  * (nar/kernels/r4_fused_v3.py:83-135, 187-201): partial[t, s*k + r] holds the
- * sum over the s-th of `splits` equal channel chunks. */
+ * sum over the s-th of `splits` equal channel chunks.  The MFMA form (rank_mode
+ * MFMA, or AUTO with k >= 16 and `prepared` given) reads `prepared` and needs
+ * n % (32*splits) == 0; the exact form reads `v`. */
 int narhip_rank_projection(const void *x_bf16, int64_t tokens, int64_t n, int64_t ld_x,
-                           const float *v, int32_t k, int32_t splits, float *partial,
-                           int32_t rank_mode, void *stream);
+                           const float *v, const void *prepared, int32_t k, int32_t splits,
+                           float *partial, int32_t rank_mode, void *stream);
 
 /* Kernel B: rotate, fold the split partials into u, subtract u W''^T, quantize.
  * Replaces nar_group_quant_kernel / launch_nar (nar/kernels/r4_fused_v2.py:
  * 155-178, 306-324; nar/kernels/r4_fused_v3.py:206-234, 251-261). */
 int narhip_group_quant(const void *x_bf16, int64_t tokens, int64_t n, int64_t ld_x,
                        int32_t had_m, int32_t had_q, const float *partial, int32_t splits,
-                       int32_t k, const float *w_t, int32_t group,
-                       uint8_t *codes, void *scales_f16, void *zeros_f16,
+                       int32_t k, const float *w_t, const void *prepared, int32_t group,
+                       uint8_t *codes, void *scales_f16, void *zeros_f16, int32_t rank_mode,
                        void *workspace, size_t workspace_bytes, void *stream);
 
 /* Dequantize packed codes: out[r, i] = q * s + z (fp32 multiply then add).
  * Replaces dequantize (nar/kernels/r4_fused_v2.py:364-369). */
 int narhip_dequantize(const uint8_t *codes, const void *scales_f16, const void *zeros_f16,
                       int64_t rows, int64_t n, int32_t group, float *out, void *stream);
+
+/* Device self-test of the MFMA operand mapping the kernels rely on (no
+ * counterpart in the reference): one v_mfma_f32_16x16x32_bf16 with
+ * a_bf16[64*8], b_bf16[64*8] per lane, d[64*4] per lane (device memory). */
+int narhip_mfma_probe(const void *a_bf16, const void *b_bf16, float *d, void *stream);
 
 #ifdef __cplusplus
 }

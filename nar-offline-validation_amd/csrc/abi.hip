@@ -2,7 +2,10 @@
 // launch.  See include/narhip.h for the contract of every entry point.
 #include "../../include/narhip.h"
 #include "narhip_device.hpp"
+#include "mfma.hpp"
 #include "rank_exact.hip"
+#include "rank_mfma.hip"
+#include "kron_mfma.hip"
 #include "rq_row.hip"
 #include "rq_seg.hip"
 #include "dequant.hip"
@@ -39,6 +42,8 @@ int check_launch(const char *what)
 
 bool pow2(int64_t v) { return v > 0 && !(v & (v - 1)); }
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
+int round_up(int v, int m) { return (v + m - 1) / m * m; }
 
 // ----------------------------------------------------------- Paley factors
 // Paley I construction: order m = p + 1 from the quadratic residues of a
@@ -113,7 +118,17 @@ PaleyTable paley_table(int m)
 
 float f32_sqrt(int v) { return (float)std::sqrt((double)v); }
 
-// ------------------------------------------------------------ dispatchers
+template <typename K>
+int set_lds(K kernel, size_t lds)
+{
+    if (lds <= 64 * 1024) return NARHIP_OK;
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return fail(NARHIP_EHIP, "hipFuncSetAttribute: %s", hipGetErrorString(e));
+    return NARHIP_OK;
+}
+
+// ------------------------------------------------------- segment kernels
 
 template <int Q, int B>
 int launch_seg_qb(const SegArgs &a, int mode, hipStream_t s)
@@ -151,50 +166,62 @@ int launch_seg(const SegArgs &a, int q, int b, int mode, hipStream_t s)
     return fail(NARHIP_EUNSUPPORTED, "segment width %d not built", q);
 }
 
+// ------------------------------------------------------ Kronecker kernels
+
 template <int M, int Q, int B>
 int launch_row_mqb(const RowArgs &a, hipStream_t s)
 {
-    if (a.T == 0) return NARHIP_OK;
     const size_t lds = sizeof(float) * M * Q;
-    static bool attr = false;
-    if (!attr) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&rq_row_kernel<M, Q, B>),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess) return fail(NARHIP_EHIP, "hipFuncSetAttribute: %s", hipGetErrorString(e));
-        attr = true;
-    }
+    if (int rc = set_lds(&rq_row_kernel<M, Q, B>, lds)) return rc;
     hipLaunchKernelGGL((rq_row_kernel<M, Q, B>), dim3((unsigned)a.T), dim3(256), lds, s, a);
     return check_launch("rq_row_kernel");
 }
 
+template <int M, int Q, int B>
+int launch_kron_mqb(const KronArgs &a, bool quant, hipStream_t s)
+{
+    const size_t lds = sizeof(float) * M * Q;
+    if (quant) {
+        if (int rc = set_lds(&kron_mfma_kernel<M, Q, B, true>, lds)) return rc;
+        hipLaunchKernelGGL((kron_mfma_kernel<M, Q, B, true>), dim3((unsigned)a.T), dim3(256), lds, s, a);
+    } else {
+        if (int rc = set_lds(&kron_mfma_kernel<M, Q, 128, false>, lds)) return rc;
+        hipLaunchKernelGGL((kron_mfma_kernel<M, Q, 128, false>), dim3((unsigned)a.T), dim3(256), lds, s, a);
+    }
+    return check_launch("kron_mfma_kernel");
+}
+
+// exact: rq_row (fp64 Paley) with RowArgs; otherwise kron_mfma with KronArgs
 template <int M, int Q>
-int launch_row_mq(const RowArgs &a, int b, hipStream_t s)
+int launch_kron_mq(const RowArgs *ra, const KronArgs *ka, bool quant, int b, hipStream_t s)
 {
     switch (b) {
-    case 32: return launch_row_mqb<M, Q, 32>(a, s);
-    case 64: return launch_row_mqb<M, Q, 64>(a, s);
-    case 128: return launch_row_mqb<M, Q, 128>(a, s);
+    case 32: return ra ? launch_row_mqb<M, Q, 32>(*ra, s) : launch_kron_mqb<M, Q, 32>(*ka, quant, s);
+    case 64: return ra ? launch_row_mqb<M, Q, 64>(*ra, s) : launch_kron_mqb<M, Q, 64>(*ka, quant, s);
+    case 128: return ra ? launch_row_mqb<M, Q, 128>(*ra, s) : launch_kron_mqb<M, Q, 128>(*ka, quant, s);
     }
     return fail(NARHIP_EUNSUPPORTED, "group %d not built", b);
 }
 
 template <int M>
-int launch_row_m(const RowArgs &a, int q, int b, hipStream_t s)
+int launch_kron_m(const RowArgs *ra, const KronArgs *ka, bool quant, int q, int b, hipStream_t s)
 {
     switch (q) {
-    case 256: return launch_row_mq<M, 256>(a, b, s);
-    case 512: return launch_row_mq<M, 512>(a, b, s);
-    case 1024: return launch_row_mq<M, 1024>(a, b, s);
+    case 256: return launch_kron_mq<M, 256>(ra, ka, quant, b, s);
+    case 512: return launch_kron_mq<M, 512>(ra, ka, quant, b, s);
+    case 1024: return launch_kron_mq<M, 1024>(ra, ka, quant, b, s);
     }
     return fail(NARHIP_EUNSUPPORTED, "Kronecker H_%d x H_%d not built", M, q);
 }
 
-int launch_row(const RowArgs &a, int m, int q, int b, hipStream_t s)
+int launch_kron(const RowArgs *ra, const KronArgs *ka, bool quant, int m, int q, int b, hipStream_t s)
 {
-    if (m == 12) return launch_row_m<12>(a, q, b, s);
-    if (m == 28) return launch_row_m<28>(a, q, b, s);
+    if (m == 12) return launch_kron_m<12>(ra, ka, quant, q, b, s);
+    if (m == 28) return launch_kron_m<28>(ra, ka, quant, q, b, s);
     return fail(NARHIP_EUNSUPPORTED, "Paley order %d not built", m);
 }
+
+// ------------------------------------------------------------ rank kernels
 
 int launch_proj_exact(const uint16_t *x, int64_t T, int64_t n, int64_t ldx, const float *v,
                       int k, int splits, float *partial, hipStream_t s)
@@ -214,16 +241,97 @@ int launch_corr_exact(const float *partial, int splits, int k, const float *wt, 
     return check_launch("corr_exact_kernel");
 }
 
+// Prepared factor layout: vt [3][kp16][n] bf16, then wtt [3][n][kp32] bf16.
+int kp16(int k) { return round_up(k < 1 ? 1 : k, 16); }
+int kp32(int k) { return round_up(k < 1 ? 1 : k, 32); }
+size_t vt_bytes(int64_t n, int k) { return align256(sizeof(uint16_t) * 3 * (size_t)kp16(k) * (size_t)n); }
+size_t wtt_bytes(int64_t n, int k) { return align256(sizeof(uint16_t) * 3 * (size_t)kp32(k) * (size_t)n); }
+size_t prepared_bytes(int64_t n, int k) { return vt_bytes(n, k) + wtt_bytes(n, k); }
+
+int launch_prepare(const float *v, const float *wt, int64_t n, int k, void *prep, hipStream_t s)
+{
+    __bf16 *vt = static_cast<__bf16 *>(prep);
+    __bf16 *wtt = reinterpret_cast<__bf16 *>(static_cast<char *>(prep) + vt_bytes(n, k));
+    if (v) {
+        const int64_t nv = n * kp16(k);
+        hipLaunchKernelGGL(prep_v_kernel, dim3((unsigned)((nv + 255) / 256)), dim3(256), 0, s, v, n, k, kp16(k), vt);
+        if (int rc = check_launch("prep_v_kernel")) return rc;
+    }
+    if (wt) {
+        const int64_t nw = n * kp32(k);
+        hipLaunchKernelGGL(prep_w_kernel, dim3((unsigned)((nw + 255) / 256)), dim3(256), 0, s, wt, n, k, kp32(k), wtt);
+        if (int rc = check_launch("prep_w_kernel")) return rc;
+    }
+    return NARHIP_OK;
+}
+
+// Channel splits for the MFMA projection: enough workgroups to cover the GPU.
+int mfma_splits(int64_t T, int64_t n)
+{
+    const int64_t tiles = (T + 63) / 64;
+    int s = 1;
+    while (s < 32 && tiles * s < 1024 && n % (64 * s) == 0) s *= 2;
+    return s;
+}
+
+int launch_proj_mfma(const uint16_t *x, int64_t T, int64_t n, int64_t ldx, const void *prep, int k, int splits,
+                     float *partial, hipStream_t s)
+{
+    if (T == 0) return NARHIP_OK;
+    if (n % (32 * (int64_t)splits)) return fail(NARHIP_EUNSUPPORTED, "MFMA projection needs n %% (32*splits) == 0");
+    ProjMfmaArgs a{x, ldx, T, n, static_cast<const __bf16 *>(prep), kp16(k), k, splits, n / splits, partial};
+    dim3 grid((unsigned)((T + 63) / 64), (unsigned)splits);
+    switch (kp16(k) / 16) {
+    case 1: hipLaunchKernelGGL((proj_mfma_kernel<1, 4>), grid, dim3(256), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((proj_mfma_kernel<2, 4>), grid, dim3(256), 0, s, a); break;
+    case 3: hipLaunchKernelGGL((proj_mfma_kernel<3, 2>), grid, dim3(256), 0, s, a); break;
+    case 4: hipLaunchKernelGGL((proj_mfma_kernel<4, 2>), grid, dim3(256), 0, s, a); break;
+    default: return fail(NARHIP_EUNSUPPORTED, "rank %d", k);
+    }
+    return check_launch("proj_mfma_kernel");
+}
+
+template <int B>
+int launch_cq_b(const CorrQuantArgs &a, int ks, dim3 grid, hipStream_t s)
+{
+    if (ks == 1) hipLaunchKernelGGL((corr_quant_kernel<B, 1>), grid, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((corr_quant_kernel<B, 2>), grid, dim3(256), 0, s, a);
+    return check_launch("corr_quant_kernel");
+}
+
+int launch_corr_quant(CorrQuantArgs a, int b, hipStream_t s)
+{
+    if (a.T == 0) return NARHIP_OK;
+    int64_t cw = 1024;
+    while (cw > 128 && a.n % cw) cw /= 2;
+    if (a.n % cw) return fail(NARHIP_EUNSUPPORTED, "rank correction needs n %% 128 == 0");
+    a.cw = cw;
+    dim3 grid((unsigned)((a.T + 63) / 64), (unsigned)(a.n / cw));
+    const int ks = a.kp / 32;
+    switch (b) {
+    case 32: return launch_cq_b<32>(a, ks, grid, s);
+    case 64: return launch_cq_b<64>(a, ks, grid, s);
+    case 128: return launch_cq_b<128>(a, ks, grid, s);
+    }
+    return fail(NARHIP_EUNSUPPORTED, "group %d not built", b);
+}
+
+// --------------------------------------------------------------- planning
+
+enum Path { PATH_SEG, PATH_SEG_PARTIAL_EXACT, PATH_KRON_EXACT, PATH_KRON_MFMA_QUANT, PATH_MFMA_RANK };
+
 struct Plan {
-    bool kron;          // row kernel (H_m (x) H_q over the row)
-    int seg_mode;       // rq_seg rank mode
-    bool need_proj;     // projection computed into the workspace
-    bool need_corr;     // correction materialised into the workspace
-    size_t proj_bytes, corr_bytes;
+    Path path;
+    bool kron;
+    int seg_mode;
+    bool need_prep, need_proj, need_P, need_corr;
+    int splits;
+    size_t prep_b, proj_b, P_b, corr_b;
+    size_t total() const { return align256(prep_b) + align256(proj_b) + align256(P_b) + align256(corr_b); }
 };
 
 int make_plan(int64_t T, int64_t n, int m, int q, int k, int64_t nb, bool have_partial, int splits,
-              int rank_mode, Plan &p)
+              bool have_prepared, int rank_mode, Plan &p)
 {
     if (T < 0 || n <= 0) return fail(NARHIP_EINVAL, "tokens %lld / n %lld invalid", (long long)T, (long long)n);
     if (!pow2(q) || q < 128 || q > 1024)
@@ -236,75 +344,139 @@ int make_plan(int64_t T, int64_t n, int m, int q, int k, int64_t nb, bool have_p
     if (rank_mode < 0 || rank_mode > 2) return fail(NARHIP_EINVAL, "rank_mode %d", rank_mode);
     p = Plan{};
     p.kron = m > 1;
-    if (k == 0) { p.seg_mode = RANK_NONE; return NARHIP_OK; }
+    const bool exact = rank_mode == NARHIP_RANK_EXACT;
+    if (k == 0) {
+        p.path = p.kron ? (exact ? PATH_KRON_EXACT : PATH_KRON_MFMA_QUANT) : PATH_SEG;
+        p.seg_mode = RANK_NONE;
+        return NARHIP_OK;
+    }
     if (nb != n && !(nb == q && m == 1))
         return fail(NARHIP_EUNSUPPORTED, "rank_block %lld: need n or the Hadamard block width", (long long)nb);
     if (nb == q && m == 1 && nb != n) {
         if (k > 8) return fail(NARHIP_EUNSUPPORTED, "per-block rank k=%d > 8", k);
         if (have_partial) return fail(NARHIP_EINVAL, "partials are only defined for a full-row rank block");
+        p.path = PATH_SEG;
         p.seg_mode = RANK_LOCAL;
         return NARHIP_OK;
     }
-    if (have_partial) {
-        if (splits < 1 || n % splits) return fail(NARHIP_EINVAL, "splits=%d must divide n=%lld", splits, (long long)n);
+    if (have_partial && (splits < 1 || n % splits))
+        return fail(NARHIP_EINVAL, "splits=%d must divide n=%lld", splits, (long long)n);
+    if (n % 128) return fail(NARHIP_EUNSUPPORTED, "full-row rank needs n %% 128 == 0");
+    const bool mfma = !exact && (rank_mode == NARHIP_RANK_MFMA || k >= 16);
+    if (mfma) {
+        p.path = PATH_MFMA_RANK;
+        p.need_prep = !have_prepared;
+        p.prep_b = p.need_prep ? prepared_bytes(n, k) : 0;
+        p.need_proj = !have_partial;
+        p.splits = have_partial ? splits : mfma_splits(T, n);
+        p.proj_b = p.need_proj ? sizeof(float) * (size_t)T * (size_t)p.splits * (size_t)k : 0;
+        p.need_P = true;
+        p.P_b = sizeof(float) * (size_t)T * (size_t)n;
+        return NARHIP_OK;
     }
-    p.seg_mode = RANK_PARTIAL;
     p.need_proj = !have_partial;
-    p.proj_bytes = p.need_proj ? sizeof(float) * (size_t)T * (size_t)k : 0;
-    p.need_corr = p.kron;
-    p.corr_bytes = p.need_corr ? sizeof(float) * (size_t)T * (size_t)n : 0;
-    if (n % 64) return fail(NARHIP_EUNSUPPORTED, "full-row rank needs n %% 64 == 0");
+    p.splits = have_partial ? splits : 1;
+    p.proj_b = p.need_proj ? sizeof(float) * (size_t)T * (size_t)k : 0;
+    if (p.kron) {
+        p.path = PATH_KRON_EXACT;
+        p.need_corr = true;
+        p.corr_b = sizeof(float) * (size_t)T * (size_t)n;
+    } else {
+        p.path = PATH_SEG_PARTIAL_EXACT;
+        p.seg_mode = RANK_PARTIAL;
+    }
     return NARHIP_OK;
 }
 
-size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
-
 int run_rotate_quant(const void *x_bf16, int64_t T, int64_t n, int64_t ldx, int m, int q, const float *signs,
-                     int k, int64_t nb, const float *v, const float *wt, const float *partial, int splits,
-                     int group, uint8_t *codes, void *scales, void *zeros, float *rotated,
-                     const int64_t *dest, int rank_mode, void *ws, size_t ws_bytes, hipStream_t s)
+                     int k, int64_t nb, const float *v, const float *wt, const void *prepared,
+                     const float *partial, int splits, int group, uint8_t *codes, void *scales, void *zeros,
+                     float *rotated, const int64_t *dest, int rank_mode, void *ws, size_t ws_bytes, hipStream_t s)
 {
     Plan p;
-    int rc = make_plan(T, n, m, q, k, nb, partial != nullptr, splits, rank_mode, p);
+    int rc = make_plan(T, n, m, q, k, nb, partial != nullptr, splits, prepared != nullptr, rank_mode, p);
     if (rc) return rc;
     if (group != 32 && group != 64 && group != 128) return fail(NARHIP_EUNSUPPORTED, "group %d", group);
     if (q % group) return fail(NARHIP_EINVAL, "group %d must divide the Hadamard block %d", group, q);
     if (ldx < n || ldx % 8) return fail(NARHIP_EINVAL, "ld_x=%lld must be >= n and a multiple of 8", (long long)ldx);
     if (T > 0 && (!x_bf16 || !codes || !scales || !zeros)) return fail(NARHIP_EINVAL, "null tensor argument");
-    if (!aligned16(x_bf16) || !aligned16(codes) || (rotated && !aligned16(rotated)))
-        return fail(NARHIP_EINVAL, "x, codes and rotated must be 16-byte aligned");
-    if (k > 0 && (!wt || (p.need_proj && !v))) return fail(NARHIP_EINVAL, "rank factors missing");
-    const size_t need = align256(p.proj_bytes) + align256(p.corr_bytes);
+    if (!aligned16(x_bf16) || !aligned16(codes) || (rotated && !aligned16(rotated)) || !aligned16(prepared))
+        return fail(NARHIP_EINVAL, "x, codes, rotated and prepared must be 16-byte aligned");
+    if (k > 0 && p.path != PATH_SEG && !prepared && !wt) return fail(NARHIP_EINVAL, "rank factor w_t missing");
+    if (k > 0 && (p.need_proj || p.seg_mode == RANK_LOCAL) && !v && !(p.path == PATH_MFMA_RANK && prepared))
+        return fail(NARHIP_EINVAL, "rank factor v missing");
+    if (p.seg_mode == RANK_LOCAL && (!v || !wt)) return fail(NARHIP_EINVAL, "rank factors missing");
+    const size_t need = p.total();
     if (need > 0 && (!ws || ws_bytes < need))
         return fail(NARHIP_EWORKSPACE, "workspace of %zu bytes required, %zu given", need, ws_bytes);
     if (T == 0) return NARHIP_OK;
 
     char *wsp = static_cast<char *>(ws);
+    void *prep = p.need_prep ? wsp : const_cast<void *>(prepared);
+    wsp += align256(p.prep_b);
     float *proj = p.need_proj ? reinterpret_cast<float *>(wsp) : nullptr;
-    float *corr = p.need_corr ? reinterpret_cast<float *>(wsp + align256(p.proj_bytes)) : nullptr;
+    wsp += align256(p.proj_b);
+    float *Pbuf = p.need_P ? reinterpret_cast<float *>(wsp) : nullptr;
+    wsp += align256(p.P_b);
+    float *corr = p.need_corr ? reinterpret_cast<float *>(wsp) : nullptr;
+    const uint16_t *x = static_cast<const uint16_t *>(x_bf16);
+
+    if (p.path == PATH_MFMA_RANK) {
+        if (p.need_prep && (rc = launch_prepare(v, wt, n, k, prep, s))) return rc;
+        const float *part = partial;
+        int sp = splits;
+        if (p.need_proj) {
+            if ((rc = launch_proj_mfma(x, T, n, ldx, prep, k, p.splits, proj, s))) return rc;
+            part = proj;
+            sp = p.splits;
+        }
+        if (p.kron) {
+            KronArgs ka{};
+            ka.x = x; ka.ldx = ldx; ka.T = T; ka.n = n; ka.signs = signs; ka.P = Pbuf;
+            ka.paley = paley_table(m); ka.sq = f32_sqrt(q); ka.hm = 1.0f / f32_sqrt(m);
+            if ((rc = launch_kron(nullptr, &ka, false, m, q, group, s))) return rc;
+        } else {
+            SegArgs sa{};
+            sa.x = x; sa.ldx = ldx; sa.T = T; sa.n = n; sa.signs = signs; sa.k = 0;
+            sa.codes = nullptr; sa.rotated = Pbuf; sa.sq = f32_sqrt(q);
+            if ((rc = launch_seg(sa, q, group, RANK_NONE, s))) return rc;
+        }
+        CorrQuantArgs ca{};
+        ca.P = Pbuf; ca.T = T; ca.n = n; ca.partial = part; ca.splits = sp; ca.k = k;
+        ca.wtt = reinterpret_cast<const __bf16 *>(static_cast<const char *>(prep) + vt_bytes(n, k));
+        ca.kp = kp32(k);
+        ca.codes = codes; ca.scales = static_cast<uint16_t *>(scales); ca.zeros = static_cast<uint16_t *>(zeros);
+        ca.dest = dest; ca.rotated = rotated;
+        return launch_corr_quant(ca, group, s);
+    }
+
     const float *part = partial;
     int sp = splits;
     if (p.need_proj) {
-        rc = launch_proj_exact(static_cast<const uint16_t *>(x_bf16), T, n, ldx, v, k, 1, proj, s);
-        if (rc) return rc;
+        if ((rc = launch_proj_exact(x, T, n, ldx, v, k, 1, proj, s))) return rc;
         part = proj;
         sp = 1;
     }
     if (p.kron) {
-        if (k > 0) {
-            rc = launch_corr_exact(part, sp, k, wt, T, n, corr, s);
-            if (rc) return rc;
+        if (k > 0 && (rc = launch_corr_exact(part, sp, k, wt, T, n, corr, s))) return rc;
+        if (p.path == PATH_KRON_MFMA_QUANT) {
+            KronArgs ka{};
+            ka.x = x; ka.ldx = ldx; ka.T = T; ka.n = n; ka.signs = signs;
+            ka.codes = codes; ka.scales = static_cast<uint16_t *>(scales); ka.zeros = static_cast<uint16_t *>(zeros);
+            ka.dest = dest; ka.rotated = rotated;
+            ka.paley = paley_table(m); ka.sq = f32_sqrt(q); ka.hm = 1.0f / f32_sqrt(m);
+            return launch_kron(nullptr, &ka, true, m, q, group, s);
         }
         RowArgs a{};
-        a.x = static_cast<const uint16_t *>(x_bf16); a.ldx = ldx; a.T = T; a.n = n;
+        a.x = x; a.ldx = ldx; a.T = T; a.n = n;
         a.signs = signs; a.corr = k > 0 ? corr : nullptr;
         a.codes = codes; a.scales = static_cast<uint16_t *>(scales); a.zeros = static_cast<uint16_t *>(zeros);
         a.dest = dest; a.rotated = rotated; a.paley = paley_table(m);
         a.sq = f32_sqrt(q); a.hm = 1.0f / f32_sqrt(m);
-        return launch_row(a, m, q, group, s);
+        return launch_kron(&a, nullptr, true, m, q, group, s);
     }
     SegArgs a{};
-    a.x = static_cast<const uint16_t *>(x_bf16); a.ldx = ldx; a.T = T; a.n = n;
+    a.x = x; a.ldx = ldx; a.T = T; a.n = n;
     a.signs = signs; a.v = v; a.wt = wt; a.partial = part; a.splits = sp; a.k = k;
     a.codes = codes; a.scales = static_cast<uint16_t *>(scales); a.zeros = static_cast<uint16_t *>(zeros);
     a.dest = dest; a.rotated = rotated; a.sq = f32_sqrt(q);
@@ -328,53 +500,80 @@ int narhip_paley(int32_t m, int8_t *out_host)
     return NARHIP_OK;
 }
 
+size_t narhip_rank_factors_bytes(int64_t n, int32_t k)
+{
+    if (n <= 0 || k < 1 || k > 64) return 0;
+    return prepared_bytes(n, k);
+}
+
+int narhip_prepare_rank_factors(const float *v, const float *w_t, int64_t n, int32_t k, void *prepared,
+                                size_t prepared_bytes_given, void *stream)
+{
+    g_error.clear();
+    if (n <= 0 || k < 1 || k > 64) return fail(NARHIP_EINVAL, "bad shape n=%lld k=%d", (long long)n, k);
+    if (!prepared || !aligned16(prepared)) return fail(NARHIP_EINVAL, "prepared buffer missing or misaligned");
+    if (prepared_bytes_given < prepared_bytes(n, k))
+        return fail(NARHIP_EWORKSPACE, "prepared buffer of %zu bytes required", prepared_bytes(n, k));
+    if (!v && !w_t) return fail(NARHIP_EINVAL, "no factor given");
+    return launch_prepare(v, w_t, n, k, prepared, static_cast<hipStream_t>(stream));
+}
+
 size_t narhip_rotate_quant_workspace(int64_t tokens, int64_t n, int32_t had_m, int32_t had_q, int32_t k,
-                                     int64_t rank_block, int32_t have_partial, int32_t splits, int32_t rank_mode)
+                                     int64_t rank_block, int32_t have_partial, int32_t splits,
+                                     int32_t have_prepared, int32_t rank_mode)
 {
     Plan p;
-    if (make_plan(tokens, n, had_m, had_q, k, rank_block, have_partial != 0, splits, rank_mode, p)) return 0;
-    return align256(p.proj_bytes) + align256(p.corr_bytes);
+    if (make_plan(tokens, n, had_m, had_q, k, rank_block, have_partial != 0, splits, have_prepared != 0,
+                  rank_mode, p))
+        return 0;
+    return p.total();
 }
 
 int narhip_rotate_quant(const void *x_bf16, int64_t tokens, int64_t n, int64_t ld_x,
                         int32_t had_m, int32_t had_q, const float *signs,
-                        int32_t k, int64_t rank_block, const float *v, const float *w_t,
+                        int32_t k, int64_t rank_block, const float *v, const float *w_t, const void *prepared,
                         const float *partial, int32_t splits,
                         int32_t group, uint8_t *codes, void *scales_f16, void *zeros_f16,
                         float *rotated, const int64_t *dest_rows, int32_t rank_mode,
                         void *workspace, size_t workspace_bytes, void *stream)
 {
     g_error.clear();
-    return run_rotate_quant(x_bf16, tokens, n, ld_x, had_m, had_q, signs, k, rank_block, v, w_t, partial,
-                            splits, group, codes, scales_f16, zeros_f16, rotated, dest_rows, rank_mode,
+    return run_rotate_quant(x_bf16, tokens, n, ld_x, had_m, had_q, signs, k, rank_block, v, w_t, prepared,
+                            partial, splits, group, codes, scales_f16, zeros_f16, rotated, dest_rows, rank_mode,
                             workspace, workspace_bytes, static_cast<hipStream_t>(stream));
 }
 
 int narhip_rank_projection(const void *x_bf16, int64_t tokens, int64_t n, int64_t ld_x,
-                           const float *v, int32_t k, int32_t splits, float *partial,
+                           const float *v, const void *prepared, int32_t k, int32_t splits, float *partial,
                            int32_t rank_mode, void *stream)
 {
     g_error.clear();
-    if (tokens < 0 || n <= 0 || ld_x < n) return fail(NARHIP_EINVAL, "bad shape");
+    if (tokens < 0 || n <= 0 || ld_x < n || ld_x % 8) return fail(NARHIP_EINVAL, "bad shape");
     if (k < 1 || k > 64) return fail(NARHIP_EUNSUPPORTED, "rank k=%d outside [1, 64]", k);
     if (splits < 1 || n % splits) return fail(NARHIP_EINVAL, "%lld channels do not divide into %d splits",
                                               (long long)n, splits);
     if (rank_mode < 0 || rank_mode > 2) return fail(NARHIP_EINVAL, "rank_mode %d", rank_mode);
-    if (tokens > 0 && (!x_bf16 || !v || !partial)) return fail(NARHIP_EINVAL, "null tensor argument");
+    const bool mfma = rank_mode == NARHIP_RANK_MFMA || (rank_mode == NARHIP_RANK_AUTO && k >= 16 && prepared);
+    if (tokens > 0 && (!x_bf16 || !partial || (mfma ? !prepared : !v)))
+        return fail(NARHIP_EINVAL, "null tensor argument");
+    if (!aligned16(x_bf16) || !aligned16(prepared)) return fail(NARHIP_EINVAL, "x and prepared must be 16-byte aligned");
+    if (mfma)
+        return launch_proj_mfma(static_cast<const uint16_t *>(x_bf16), tokens, n, ld_x, prepared, k, splits, partial,
+                                static_cast<hipStream_t>(stream));
     return launch_proj_exact(static_cast<const uint16_t *>(x_bf16), tokens, n, ld_x, v, k, splits, partial,
                              static_cast<hipStream_t>(stream));
 }
 
 int narhip_group_quant(const void *x_bf16, int64_t tokens, int64_t n, int64_t ld_x,
                        int32_t had_m, int32_t had_q, const float *partial, int32_t splits,
-                       int32_t k, const float *w_t, int32_t group,
-                       uint8_t *codes, void *scales_f16, void *zeros_f16,
+                       int32_t k, const float *w_t, const void *prepared, int32_t group,
+                       uint8_t *codes, void *scales_f16, void *zeros_f16, int32_t rank_mode,
                        void *workspace, size_t workspace_bytes, void *stream)
 {
     g_error.clear();
     if (k > 0 && !partial) return fail(NARHIP_EINVAL, "partials required");
-    return run_rotate_quant(x_bf16, tokens, n, ld_x, had_m, had_q, nullptr, k, n, nullptr, w_t, partial, splits,
-                            group, codes, scales_f16, zeros_f16, nullptr, nullptr, NARHIP_RANK_EXACT,
+    return run_rotate_quant(x_bf16, tokens, n, ld_x, had_m, had_q, nullptr, k, n, nullptr, w_t, prepared, partial,
+                            splits, group, codes, scales_f16, zeros_f16, nullptr, nullptr, rank_mode,
                             workspace, workspace_bytes, static_cast<hipStream_t>(stream));
 }
 
@@ -393,6 +592,15 @@ int narhip_dequantize(const uint8_t *codes, const void *scales_f16, const void *
                        static_cast<hipStream_t>(stream), codes, static_cast<const uint16_t *>(scales_f16),
                        static_cast<const uint16_t *>(zeros_f16), rows, n, group, out);
     return check_launch("dequant_kernel");
+}
+
+int narhip_mfma_probe(const void *a_bf16, const void *b_bf16, float *d, void *stream)
+{
+    g_error.clear();
+    if (!a_bf16 || !b_bf16 || !d) return fail(NARHIP_EINVAL, "null argument");
+    hipLaunchKernelGGL(mfma_probe_kernel, dim3(1), dim3(64), 0, static_cast<hipStream_t>(stream),
+                       static_cast<const __bf16 *>(a_bf16), static_cast<const __bf16 *>(b_bf16), d);
+    return check_launch("mfma_probe_kernel");
 }
 
 }  // extern "C"

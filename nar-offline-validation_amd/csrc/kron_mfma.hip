@@ -1,0 +1,196 @@
+// Kronecker row transform with the Paley factor on bf16 MFMA.
+//
+// One workgroup per token (4 waves, 16 rows of 16 lanes):
+//   phase 1  F[a, :] = FWHT_Q(x[a*Q:(a+1)*Q]) / fp32(sqrt(Q))   (DPP, as rq_row.hip)
+//   phase 2  P[a, c] = hm * S[a, c],  S = Hm(+-1) F                  (MFMA)
+//            F enters as three exact bf16 terms; S1 = Hm F_hi and S23 = Hm (F_mid + F_lo)
+//            are sums of bf16 values with +-1 weights, and P = fma(hm, S1, hm*S23)
+//            is the fp32 rounding of hm*S -- the oracle's fp64 definition of the
+//            reference's BLAS product -- whenever the two sums are exact in fp32.
+//   phase 3  either the group quantizer (no rank term) or a coalesced copy of P
+//            to global memory for the rank-k correction kernel.
+#include "mfma.hpp"
+#include "narhip_device.hpp"
+
+namespace narhip {
+
+struct KronArgs {
+    const uint16_t *x;
+    int64_t ldx, T, n;
+    const float *signs;
+    float *P;              // [T, n] output when not quantizing
+    uint8_t *codes;
+    uint16_t *scales;
+    uint16_t *zeros;
+    const int64_t *dest;
+    float *rotated;
+    PaleyTable paley;
+    float sq, hm;
+};
+
+template <int M, int Q, int B, bool QUANT>
+__global__ void __launch_bounds__(256)
+kron_mfma_kernel(KronArgs a)
+{
+    constexpr int NH = Q / 128;
+    constexpr int NV = 8 * NH;
+    constexpr int N = M * Q;
+    constexpr int NMT = (M + 15) / 16;
+    extern __shared__ float F[];
+    const int tid = threadIdx.x;
+    const int l16 = tid & 15;
+    const int row = tid >> 4;
+    const int chunk = lane_chunk(l16);
+    const int64_t t = blockIdx.x;
+    const uint16_t *xt = a.x + t * a.ldx;
+
+    // ---- phase 1 (identical arithmetic to rq_row_kernel)
+    for (int s = row; s < M; s += 16) {
+        float v[NV];
+#pragma unroll
+        for (int h = 0; h < NH; h++) {
+            uint4 wv = *reinterpret_cast<const uint4 *>(xt + s * Q + h * 128 + chunk * 8);
+            v[h * 8 + 0] = bf16lo(wv.x); v[h * 8 + 1] = bf16hi(wv.x);
+            v[h * 8 + 2] = bf16lo(wv.y); v[h * 8 + 3] = bf16hi(wv.y);
+            v[h * 8 + 4] = bf16lo(wv.z); v[h * 8 + 5] = bf16hi(wv.z);
+            v[h * 8 + 6] = bf16lo(wv.w); v[h * 8 + 7] = bf16hi(wv.w);
+        }
+        if (a.signs) {
+#pragma unroll
+            for (int h = 0; h < NH; h++)
+#pragma unroll
+                for (int e = 0; e < 8; e++) v[h * 8 + e] *= a.signs[s * Q + h * 128 + chunk * 8 + e];
+        }
+#pragma unroll
+        for (int wd = 1; wd < 8; wd <<= 1)
+#pragma unroll
+            for (int h = 0; h < NH; h++)
+#pragma unroll
+                for (int e = 0; e < 8; e++)
+                    if (!(e & wd)) {
+                        float x0 = v[h * 8 + e], x1 = v[h * 8 + e + wd];
+                        v[h * 8 + e] = x0 + x1;
+                        v[h * 8 + e + wd] = x0 - x1;
+                    }
+        {
+            const float s0 = (chunk & 1) ? -1.0f : 1.0f;
+            const float s1 = (chunk & 2) ? -1.0f : 1.0f;
+            const float s2 = (chunk & 4) ? -1.0f : 1.0f;
+            const float s3 = (chunk & 8) ? -1.0f : 1.0f;
+#pragma unroll
+            for (int i = 0; i < NV; i++) v[i] = __builtin_fmaf(s0, v[i], xchg<0>(v[i]));
+#pragma unroll
+            for (int i = 0; i < NV; i++) v[i] = __builtin_fmaf(s1, v[i], xchg<1>(v[i]));
+#pragma unroll
+            for (int i = 0; i < NV; i++) v[i] = __builtin_fmaf(s2, v[i], xchg<2>(v[i]));
+#pragma unroll
+            for (int i = 0; i < NV; i++) v[i] = __builtin_fmaf(s3, v[i], xchg<3>(v[i]));
+        }
+#pragma unroll
+        for (int wh = 1; wh < NH; wh <<= 1)
+#pragma unroll
+            for (int h = 0; h < NH; h++)
+                if (!(h & wh))
+#pragma unroll
+                    for (int e = 0; e < 8; e++) {
+                        float x0 = v[h * 8 + e], x1 = v[(h + wh) * 8 + e];
+                        v[h * 8 + e] = x0 + x1;
+                        v[(h + wh) * 8 + e] = x0 - x1;
+                    }
+        const float sq = a.sq;
+#pragma unroll
+        for (int h = 0; h < NH; h++) {
+            float4 *d = reinterpret_cast<float4 *>(F + s * Q + h * 128 + chunk * 8);
+            d[0] = make_float4(v[h * 8 + 0] / sq, v[h * 8 + 1] / sq, v[h * 8 + 2] / sq, v[h * 8 + 3] / sq);
+            d[1] = make_float4(v[h * 8 + 4] / sq, v[h * 8 + 5] / sq, v[h * 8 + 6] / sq, v[h * 8 + 7] / sq);
+        }
+    }
+    __syncthreads();
+
+    // ---- phase 2: Paley product on MFMA, one 16-column block at a time, in place
+    {
+        const int lane = tid & 63, wv = tid >> 6;
+        const int g = lane >> 4, c16 = lane & 15;
+        bf16x8 ha[NMT];
+#pragma unroll
+        for (int mt = 0; mt < NMT; mt++) {
+            const int r = 16 * mt + c16;
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const int c = 8 * g + j;
+                float e = 0.0f;
+                if (r < M && c < M) e = ((a.paley.neg[r] >> c) & 1u) ? -1.0f : 1.0f;
+                ha[mt][j] = (__bf16)e;
+            }
+        }
+        const float hm = a.hm;
+        constexpr int CB = Q / 16;
+        for (int cb = wv; cb < CB; cb += 4) {
+            const int c = 16 * cb + c16;
+            float f[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const int ar = 8 * g + j;
+                f[j] = ar < M ? F[ar * Q + c] : 0.0f;
+            }
+            bf16x8 bh, bm, bl;
+            split3x8(f, bh, bm, bl);
+#pragma unroll
+            for (int mt = 0; mt < NMT; mt++) {
+                const floatx4 s1 = mfma_bf16(ha[mt], bh, zero4());
+                floatx4 s2 = mfma_bf16(ha[mt], bm, zero4());
+                s2 = mfma_bf16(ha[mt], bl, s2);
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int ar = 16 * mt + 4 * g + i;
+                    if (ar < M) F[ar * Q + c] = __builtin_fmaf(hm, s1[i], hm * s2[i]);
+                }
+            }
+        }
+    }
+    __syncthreads();
+
+    if constexpr (!QUANT) {
+        float4 *dst = reinterpret_cast<float4 *>(a.P + t * N);
+        for (int i = tid; i < N / 4; i += 256) dst[i] = reinterpret_cast<const float4 *>(F)[i];
+        return;
+    } else {
+        if (a.rotated) {
+            for (int i = tid; i < N / 4; i += 256)
+                reinterpret_cast<float4 *>(a.rotated + t * N)[i] = reinterpret_cast<const float4 *>(F)[i];
+        }
+        constexpr int G8 = B / 8;
+        constexpr int CHUNKS = N / 8;
+        const int64_t orow = a.dest ? a.dest[t] : t;
+        for (int c0 = 0; c0 < CHUNKS; c0 += 256) {
+            const int ch = c0 + tid;
+            const bool ok = ch < CHUNKS;
+            const int chs = ok ? ch : 0;
+            float v[8];
+            {
+                const float4 *s = reinterpret_cast<const float4 *>(F + chs * 8);
+                float4 p0 = s[0], p1 = s[1];
+                v[0] = p0.x; v[1] = p0.y; v[2] = p0.z; v[3] = p0.w;
+                v[4] = p1.x; v[5] = p1.y; v[6] = p1.z; v[7] = p1.w;
+            }
+            float lo = v[0], hi = v[0];
+#pragma unroll
+            for (int e = 1; e < 8; e++) { lo = fminf(lo, v[e]); hi = fmaxf(hi, v[e]); }
+            group_minmax<G8>(lo, hi);
+            const GroupParams gp = group_params(lo, hi);
+            uint32_t word = 0;
+#pragma unroll
+            for (int e = 0; e < 8; e++) word |= quant_code(v[e], gp) << (4 * e);
+            if (ok) {
+                *reinterpret_cast<uint32_t *>(a.codes + orow * (N / 2) + ch * 4) = word;
+                if ((ch % G8) == 0) {
+                    const int64_t gi = orow * (N / B) + (ch * 8) / B;
+                    a.scales[gi] = gp.s16;
+                    a.zeros[gi] = gp.z16;
+                }
+            }
+        }
+    }
+}
+
+}  // namespace narhip

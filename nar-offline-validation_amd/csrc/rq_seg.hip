@@ -175,7 +175,8 @@ rq_seg_kernel(SegArgs a)
         }
     }
 
-    // ---- quantize groups of B and store
+    // ---- quantize groups of B and store (codes == null: rotation only, into `rotated`)
+    if (!a.codes) return;
     const int64_t orow = a.dest ? a.dest[t] : t;
     const int64_t gpt = a.n / B;   // groups per token
 #pragma unroll

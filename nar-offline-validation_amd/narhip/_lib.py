@@ -24,7 +24,9 @@ RANK_MFMA = 2
 EXPORTS = (
     "narhip_abi_version", "narhip_last_error_string", "narhip_paley",
     "narhip_rotate_quant", "narhip_rotate_quant_workspace",
+    "narhip_rank_factors_bytes", "narhip_prepare_rank_factors",
     "narhip_rank_projection", "narhip_group_quant", "narhip_dequantize",
+    "narhip_mfma_probe",
 )
 
 _lib: ctypes.CDLL | None = None
@@ -44,17 +46,22 @@ def load() -> ctypes.CDLL:
     lib.narhip_paley.argtypes = [c_i32, c_p]
     lib.narhip_rotate_quant.argtypes = [
         c_p, c_i64, c_i64, c_i64, c_i32, c_i32, c_p,
-        c_i32, c_i64, c_p, c_p, c_p, c_i32,
+        c_i32, c_i64, c_p, c_p, c_p, c_p, c_i32,
         c_i32, c_p, c_p, c_p, c_p, c_p, c_i32, c_p, c_sz, c_p]
-    lib.narhip_rotate_quant_workspace.argtypes = [c_i64, c_i64, c_i32, c_i32, c_i32, c_i64, c_i32, c_i32, c_i32]
+    lib.narhip_rotate_quant_workspace.argtypes = [c_i64, c_i64, c_i32, c_i32, c_i32, c_i64, c_i32, c_i32,
+                                                  c_i32, c_i32]
     lib.narhip_rotate_quant_workspace.restype = c_sz
-    lib.narhip_rank_projection.argtypes = [c_p, c_i64, c_i64, c_i64, c_p, c_i32, c_i32, c_p, c_i32, c_p]
+    lib.narhip_rank_factors_bytes.argtypes = [c_i64, c_i32]
+    lib.narhip_rank_factors_bytes.restype = c_sz
+    lib.narhip_prepare_rank_factors.argtypes = [c_p, c_p, c_i64, c_i32, c_p, c_sz, c_p]
+    lib.narhip_rank_projection.argtypes = [c_p, c_i64, c_i64, c_i64, c_p, c_p, c_i32, c_i32, c_p, c_i32, c_p]
     lib.narhip_group_quant.argtypes = [
-        c_p, c_i64, c_i64, c_i64, c_i32, c_i32, c_p, c_i32, c_i32, c_p, c_i32,
-        c_p, c_p, c_p, c_p, c_sz, c_p]
+        c_p, c_i64, c_i64, c_i64, c_i32, c_i32, c_p, c_i32, c_i32, c_p, c_p, c_i32,
+        c_p, c_p, c_p, c_i32, c_p, c_sz, c_p]
     lib.narhip_dequantize.argtypes = [c_p, c_p, c_p, c_i64, c_i64, c_i32, c_p, c_p]
-    for name in ("narhip_paley", "narhip_rotate_quant", "narhip_rank_projection",
-                 "narhip_group_quant", "narhip_dequantize"):
+    lib.narhip_mfma_probe.argtypes = [c_p, c_p, c_p, c_p]
+    for name in ("narhip_paley", "narhip_rotate_quant", "narhip_rank_projection", "narhip_prepare_rank_factors",
+                 "narhip_group_quant", "narhip_dequantize", "narhip_mfma_probe"):
         getattr(lib, name).restype = ctypes.c_int
     _lib = lib
     return lib

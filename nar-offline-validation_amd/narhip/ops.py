@@ -55,9 +55,32 @@ def paley(m: int) -> torch.Tensor:
     return out
 
 
+def prepare_rank_factors(v: torch.Tensor | None, w_t: torch.Tensor | None, n: int, k: int,
+                         out: torch.Tensor | None = None) -> torch.Tensor:
+    """V and W''^T as exact bf16 term triples in the MFMA layouts (uint8 buffer).
+
+    Done once per factor set, like the reference's term padding in
+    FoldedR4.from_factor / NARDownTransform.__init__."""
+    ref = v if v is not None else w_t
+    dev = ref.device
+    if v is not None:
+        _require(v, torch.float32, "v", dev)
+    if w_t is not None:
+        _require(w_t, torch.float32, "w_t", dev)
+    lib = _lib.load()
+    nbytes = lib.narhip_rank_factors_bytes(n, k)
+    if nbytes == 0:
+        raise ValueError(f"no prepared layout for n={n}, k={k}")
+    if out is None:
+        out = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    _lib.check(lib.narhip_prepare_rank_factors(_p(v), _p(w_t), n, k, _p(out), out.numel(), _stream(dev)))
+    return out
+
+
 def rotate_quant(x: torch.Tensor, *, hadamard: tuple[int, int] = (1, 128),
                  signs: torch.Tensor | None = None,
                  v: torch.Tensor | None = None, w_t: torch.Tensor | None = None,
+                 prepared: torch.Tensor | None = None,
                  rank_block: int | None = None,
                  partial: torch.Tensor | None = None,
                  group: int = 128,
@@ -116,38 +139,44 @@ def rotate_quant(x: torch.Tensor, *, hadamard: tuple[int, int] = (1, 128),
         _require(dest_rows, torch.int64, "dest_rows", dev)
     nb = n if rank_block is None else int(rank_block)
     lib = _lib.load()
-    ws_bytes = lib.narhip_rotate_quant_workspace(T, n, m, q, k, nb, int(partial is not None), splits, rank_mode)
+    ws_bytes = lib.narhip_rotate_quant_workspace(T, n, m, q, k, nb, int(partial is not None), splits,
+                                                 int(prepared is not None), rank_mode)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
     rc = lib.narhip_rotate_quant(
-        _p(x), T, n, x.stride(0), m, q, _p(signs), k, nb, _p(v), _p(w_t), _p(partial), splits,
+        _p(x), T, n, x.stride(0), m, q, _p(signs), k, nb, _p(v), _p(w_t), _p(prepared), _p(partial), splits,
         group, _p(codes), _p(scales), _p(zeros), _p(rotated), _p(dest_rows), rank_mode,
         _p(ws), ws_bytes, _stream(dev))
     _lib.check(rc)
     return codes, scales, zeros
 
 
-def rank_projection(x: torch.Tensor, v: torch.Tensor, partial: torch.Tensor,
-                    rank_mode: int = RANK_AUTO) -> torch.Tensor:
+def rank_projection(x: torch.Tensor, v: torch.Tensor | None, partial: torch.Tensor,
+                    rank_mode: int = RANK_AUTO, *, prepared: torch.Tensor | None = None,
+                    k: int | None = None) -> torch.Tensor:
     """partial[t, s*k + r] = sum over channel split s of x[t, i] v[i, r]."""
     if x.dtype != torch.bfloat16 or x.stride(1) != 1:
         raise ValueError("x must be bfloat16 with contiguous rows")
     dev = x.device
-    _require(v, torch.float32, "v", dev)
+    if v is not None:
+        _require(v, torch.float32, "v", dev)
+        k = int(v.shape[1])
+    if k is None:
+        raise ValueError("rank k unknown: pass v or k")
     _require(partial, torch.float32, "partial", dev)
     T, n = x.shape
-    k = int(v.shape[1])
     if partial.shape[0] != T or partial.shape[1] % k:
         raise ValueError("partial must be [tokens, splits*k]")
     splits = partial.shape[1] // k
-    rc = _lib.load().narhip_rank_projection(_p(x), T, n, x.stride(0), _p(v), k, splits, _p(partial),
-                                            rank_mode, _stream(dev))
+    rc = _lib.load().narhip_rank_projection(_p(x), T, n, x.stride(0), _p(v), _p(prepared), k, splits,
+                                            _p(partial), rank_mode, _stream(dev))
     _lib.check(rc)
     return partial
 
 
 def group_quant(x: torch.Tensor, partial: torch.Tensor | None, w_t: torch.Tensor | None,
                 codes: torch.Tensor, scales: torch.Tensor, zeros: torch.Tensor, *,
-                hadamard: tuple[int, int] = (1, 128), group: int = 128) -> None:
+                hadamard: tuple[int, int] = (1, 128), group: int = 128,
+                prepared: torch.Tensor | None = None, rank_mode: int = RANK_AUTO) -> None:
     """Kernel B: rotate, fold the split partials, subtract u W^T, quantize."""
     if x.dtype != torch.bfloat16 or x.stride(1) != 1:
         raise ValueError("x must be bfloat16 with contiguous rows")
@@ -161,10 +190,11 @@ def group_quant(x: torch.Tensor, partial: torch.Tensor | None, w_t: torch.Tensor
         splits = partial.shape[1] // k
     m, q = hadamard
     lib = _lib.load()
-    ws_bytes = lib.narhip_rotate_quant_workspace(T, n, m, q, k, n, 1, splits, RANK_EXACT)
+    ws_bytes = lib.narhip_rotate_quant_workspace(T, n, m, q, k, n, 1, splits, int(prepared is not None), rank_mode)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
-    rc = lib.narhip_group_quant(_p(x), T, n, x.stride(0), m, q, _p(partial), splits, k, _p(w_t), group,
-                                _p(codes), _p(scales), _p(zeros), _p(ws), ws_bytes, _stream(dev))
+    rc = lib.narhip_group_quant(_p(x), T, n, x.stride(0), m, q, _p(partial), splits, k, _p(w_t), _p(prepared),
+                                group, _p(codes), _p(scales), _p(zeros), rank_mode, _p(ws), ws_bytes,
+                                _stream(dev))
     _lib.check(rc)
 
 
@@ -179,6 +209,16 @@ def dequantize(codes: torch.Tensor, scales: torch.Tensor, zeros: torch.Tensor, n
     _lib.check(_lib.load().narhip_dequantize(_p(codes), _p(scales), _p(zeros), rows, n, group,
                                              _p(out), _stream(dev)))
     return out
+
+
+def mfma_probe(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """One v_mfma_f32_16x16x32_bf16 on per-lane operands a, b (bf16 [64, 8]) -> fp32 [64, 4]."""
+    dev = a.device
+    _require(a, torch.bfloat16, "a", dev)
+    _require(b, torch.bfloat16, "b", dev)
+    d = torch.empty((64, 4), dtype=torch.float32, device=dev)
+    _lib.check(_lib.load().narhip_mfma_probe(_p(a), _p(b), _p(d), _stream(dev)))
+    return d
 
 
 def sqrt_f32(v: int) -> float:

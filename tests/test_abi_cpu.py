@@ -48,7 +48,7 @@ def test_unsupported_paley_order():
 
 def _rq(lib, **kw):
     a = dict(x=None, T=4, n=1024, ld=1024, m=1, q=128, signs=None, k=0, nb=1024, v=None, wt=None,
-             partial=None, splits=0, group=128, codes=None, scales=None, zeros=None, rot=None,
+             prepared=None, partial=None, splits=0, group=128, codes=None, scales=None, zeros=None, rot=None,
              dest=None, mode=0, ws=None, wsb=0, stream=None)
     a.update(kw)
     return lib.narhip_rotate_quant(*a.values())
@@ -75,9 +75,12 @@ def test_host_validation(kw, code):
 def test_workspace_query():
     import narhip
     lib = narhip.load()
-    assert lib.narhip_rotate_quant_workspace(8, 1024, 1, 128, 0, 1024, 0, 0, 0) == 0
-    ws = lib.narhip_rotate_quant_workspace(8192, 14336, 28, 512, 32, 14336, 0, 0, 1)
-    assert ws >= 8192 * 14336 * 4
+    assert lib.narhip_rotate_quant_workspace(8, 1024, 1, 128, 0, 1024, 0, 0, 0, 0) == 0
+    exact = lib.narhip_rotate_quant_workspace(8192, 14336, 28, 512, 32, 14336, 0, 0, 0, 1)
+    assert exact >= 8192 * 14336 * 4
+    mfma = lib.narhip_rotate_quant_workspace(8192, 14336, 28, 512, 32, 14336, 0, 0, 0, 0)
+    prepared = lib.narhip_rotate_quant_workspace(8192, 14336, 28, 512, 32, 14336, 0, 0, 1, 0)
+    assert mfma - prepared == lib.narhip_rank_factors_bytes(14336, 32) > 0
 
 
 def test_hadamard_factor_dispatch_order():
