@@ -115,8 +115,8 @@ int narhip_prepare_rank_factors(const float *v, const float *w_t, int64_t n, int
  * (nar/kernels/r4_fused_v2.py:122-152, 292-303) and launch_projection_dot
  * (nar/kernels/r4_fused_v3.py:83-135, 187-201): partial[t, s*k + r] holds the
  * sum over the s-th of `splits` equal channel chunks.  The MFMA form (rank_mode
- * MFMA, or AUTO with k >= 16 and `prepared` given) reads `prepared` and needs
- * n % (32*splits) == 0; the exact form reads `v`. */
+ * MFMA, or AUTO with k >= 16, `prepared` given and n % (128*splits) == 0)
+ * reads `prepared`; the exact form reads `v`. */
 int narhip_rank_projection(const void *x_bf16, int64_t tokens, int64_t n, int64_t ld_x,
                            const float *v, const void *prepared, int32_t k, int32_t splits,
                            float *partial, int32_t rank_mode, void *stream);

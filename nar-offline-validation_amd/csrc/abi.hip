@@ -265,27 +265,32 @@ int launch_prepare(const float *v, const float *wt, int64_t n, int k, void *prep
     return NARHIP_OK;
 }
 
-// Channel splits for the MFMA projection: enough workgroups to cover the GPU.
+// Channel splits for the MFMA projection: enough workgroups to cover the GPU
+// (256-token tiles, splits of a multiple of 128 channels).
 int mfma_splits(int64_t T, int64_t n)
 {
-    const int64_t tiles = (T + 63) / 64;
+    const int64_t tiles = (T + 255) / 256;
     int s = 1;
-    while (s < 32 && tiles * s < 1024 && n % (64 * s) == 0) s *= 2;
+    while (s < 64 && tiles * s < 512 && n % (256 * (int64_t)s) == 0) s *= 2;
     return s;
 }
+
+bool mfma_projection_ok(int64_t n, int splits) { return n % (128 * (int64_t)splits) == 0; }
 
 int launch_proj_mfma(const uint16_t *x, int64_t T, int64_t n, int64_t ldx, const void *prep, int k, int splits,
                      float *partial, hipStream_t s)
 {
     if (T == 0) return NARHIP_OK;
-    if (n % (32 * (int64_t)splits)) return fail(NARHIP_EUNSUPPORTED, "MFMA projection needs n %% (32*splits) == 0");
+    if (!mfma_projection_ok(n, splits))
+        return fail(NARHIP_EUNSUPPORTED, "MFMA projection needs n %% (128*splits) == 0 (n=%lld, splits=%d)",
+                    (long long)n, splits);
     ProjMfmaArgs a{x, ldx, T, n, static_cast<const __bf16 *>(prep), kp16(k), k, splits, n / splits, partial};
-    dim3 grid((unsigned)((T + 63) / 64), (unsigned)splits);
+    dim3 grid((unsigned)((T + 255) / 256), (unsigned)splits);
     switch (kp16(k) / 16) {
-    case 1: hipLaunchKernelGGL((proj_mfma_kernel<1, 4>), grid, dim3(256), 0, s, a); break;
-    case 2: hipLaunchKernelGGL((proj_mfma_kernel<2, 4>), grid, dim3(256), 0, s, a); break;
-    case 3: hipLaunchKernelGGL((proj_mfma_kernel<3, 2>), grid, dim3(256), 0, s, a); break;
-    case 4: hipLaunchKernelGGL((proj_mfma_kernel<4, 2>), grid, dim3(256), 0, s, a); break;
+    case 1: hipLaunchKernelGGL((proj_mfma_kernel<1>), grid, dim3(256), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((proj_mfma_kernel<2>), grid, dim3(256), 0, s, a); break;
+    case 3: hipLaunchKernelGGL((proj_mfma_kernel<3>), grid, dim3(256), 0, s, a); break;
+    case 4: hipLaunchKernelGGL((proj_mfma_kernel<4>), grid, dim3(256), 0, s, a); break;
     default: return fail(NARHIP_EUNSUPPORTED, "rank %d", k);
     }
     return check_launch("proj_mfma_kernel");
@@ -320,12 +325,31 @@ int launch_corr_quant(CorrQuantArgs a, int b, hipStream_t s)
 
 enum Path { PATH_SEG, PATH_SEG_PARTIAL_EXACT, PATH_KRON_EXACT, PATH_KRON_MFMA_QUANT, PATH_MFMA_RANK };
 
+// The MFMA rank path stages the rotated rows P through memory between the
+// transform and the correction kernels; tokens are processed in chunks so that
+// the P workspace stays bounded (4 GB by default).  Chunks small enough to stay
+// resident in the 256 MB Infinity Cache were measured slower on MI355X (the
+// per-chunk launches under-fill the GPU), so the default covers every
+// benchmark shape in one chunk.
+#ifndef NARHIP_CHUNK_BYTES
+#define NARHIP_CHUNK_BYTES (4096ll << 20)
+#endif
+
+int64_t chunk_tokens(int64_t T, int64_t n)
+{
+    int64_t tc = NARHIP_CHUNK_BYTES / (n * (int64_t)sizeof(float));
+    tc = tc / 256 * 256;
+    if (tc < 256) tc = 256;
+    return tc < T ? tc : T;
+}
+
 struct Plan {
     Path path;
     bool kron;
     int seg_mode;
     bool need_prep, need_proj, need_P, need_corr;
     int splits;
+    int64_t chunk;
     size_t prep_b, proj_b, P_b, corr_b;
     size_t total() const { return align256(prep_b) + align256(proj_b) + align256(P_b) + align256(corr_b); }
 };
@@ -368,10 +392,11 @@ int make_plan(int64_t T, int64_t n, int m, int q, int k, int64_t nb, bool have_p
         p.need_prep = !have_prepared;
         p.prep_b = p.need_prep ? prepared_bytes(n, k) : 0;
         p.need_proj = !have_partial;
-        p.splits = have_partial ? splits : mfma_splits(T, n);
-        p.proj_b = p.need_proj ? sizeof(float) * (size_t)T * (size_t)p.splits * (size_t)k : 0;
+        p.chunk = chunk_tokens(T, n);
+        p.splits = have_partial ? splits : mfma_splits(p.chunk, n);
+        p.proj_b = p.need_proj ? sizeof(float) * (size_t)p.chunk * (size_t)p.splits * (size_t)k : 0;
         p.need_P = true;
-        p.P_b = sizeof(float) * (size_t)T * (size_t)n;
+        p.P_b = sizeof(float) * (size_t)p.chunk * (size_t)n;
         return NARHIP_OK;
     }
     p.need_proj = !have_partial;
@@ -423,31 +448,40 @@ int run_rotate_quant(const void *x_bf16, int64_t T, int64_t n, int64_t ldx, int 
 
     if (p.path == PATH_MFMA_RANK) {
         if (p.need_prep && (rc = launch_prepare(v, wt, n, k, prep, s))) return rc;
-        const float *part = partial;
-        int sp = splits;
-        if (p.need_proj) {
-            if ((rc = launch_proj_mfma(x, T, n, ldx, prep, k, p.splits, proj, s))) return rc;
-            part = proj;
-            sp = p.splits;
+        for (int64_t t0 = 0; t0 < T; t0 += p.chunk) {
+            const int64_t tn = T - t0 < p.chunk ? T - t0 : p.chunk;
+            const uint16_t *xc = x + t0 * ldx;
+            const float *part = partial ? partial + t0 * (int64_t)splits * k : nullptr;
+            int sp = splits;
+            if (p.need_proj) {
+                if ((rc = launch_proj_mfma(xc, tn, n, ldx, prep, k, p.splits, proj, s))) return rc;
+                part = proj;
+                sp = p.splits;
+            }
+            if (p.kron) {
+                KronArgs ka{};
+                ka.x = xc; ka.ldx = ldx; ka.T = tn; ka.n = n; ka.signs = signs; ka.P = Pbuf;
+                ka.paley = paley_table(m); ka.sq = f32_sqrt(q); ka.hm = 1.0f / f32_sqrt(m);
+                if ((rc = launch_kron(nullptr, &ka, false, m, q, group, s))) return rc;
+            } else {
+                SegArgs sa{};
+                sa.x = xc; sa.ldx = ldx; sa.T = tn; sa.n = n; sa.signs = signs; sa.k = 0;
+                sa.codes = nullptr; sa.rotated = Pbuf; sa.sq = f32_sqrt(q);
+                if ((rc = launch_seg(sa, q, group, RANK_NONE, s))) return rc;
+            }
+            CorrQuantArgs ca{};
+            ca.P = Pbuf; ca.T = tn; ca.n = n; ca.partial = part; ca.splits = sp; ca.k = k;
+            ca.wtt = reinterpret_cast<const __bf16 *>(static_cast<const char *>(prep) + vt_bytes(n, k));
+            ca.kp = kp32(k);
+            ca.dest = dest ? dest + t0 : nullptr;
+            const int64_t row0 = dest ? 0 : t0;
+            ca.codes = codes + row0 * (n / 2);
+            ca.scales = static_cast<uint16_t *>(scales) + row0 * (n / group);
+            ca.zeros = static_cast<uint16_t *>(zeros) + row0 * (n / group);
+            ca.rotated = rotated ? rotated + t0 * n : nullptr;
+            if ((rc = launch_corr_quant(ca, group, s))) return rc;
         }
-        if (p.kron) {
-            KronArgs ka{};
-            ka.x = x; ka.ldx = ldx; ka.T = T; ka.n = n; ka.signs = signs; ka.P = Pbuf;
-            ka.paley = paley_table(m); ka.sq = f32_sqrt(q); ka.hm = 1.0f / f32_sqrt(m);
-            if ((rc = launch_kron(nullptr, &ka, false, m, q, group, s))) return rc;
-        } else {
-            SegArgs sa{};
-            sa.x = x; sa.ldx = ldx; sa.T = T; sa.n = n; sa.signs = signs; sa.k = 0;
-            sa.codes = nullptr; sa.rotated = Pbuf; sa.sq = f32_sqrt(q);
-            if ((rc = launch_seg(sa, q, group, RANK_NONE, s))) return rc;
-        }
-        CorrQuantArgs ca{};
-        ca.P = Pbuf; ca.T = T; ca.n = n; ca.partial = part; ca.splits = sp; ca.k = k;
-        ca.wtt = reinterpret_cast<const __bf16 *>(static_cast<const char *>(prep) + vt_bytes(n, k));
-        ca.kp = kp32(k);
-        ca.codes = codes; ca.scales = static_cast<uint16_t *>(scales); ca.zeros = static_cast<uint16_t *>(zeros);
-        ca.dest = dest; ca.rotated = rotated;
-        return launch_corr_quant(ca, group, s);
+        return NARHIP_OK;
     }
 
     const float *part = partial;
@@ -553,7 +587,8 @@ int narhip_rank_projection(const void *x_bf16, int64_t tokens, int64_t n, int64_
     if (splits < 1 || n % splits) return fail(NARHIP_EINVAL, "%lld channels do not divide into %d splits",
                                               (long long)n, splits);
     if (rank_mode < 0 || rank_mode > 2) return fail(NARHIP_EINVAL, "rank_mode %d", rank_mode);
-    const bool mfma = rank_mode == NARHIP_RANK_MFMA || (rank_mode == NARHIP_RANK_AUTO && k >= 16 && prepared);
+    const bool mfma = rank_mode == NARHIP_RANK_MFMA ||
+                      (rank_mode == NARHIP_RANK_AUTO && k >= 16 && prepared && mfma_projection_ok(n, splits));
     if (tokens > 0 && (!x_bf16 || !partial || (mfma ? !prepared : !v)))
         return fail(NARHIP_EINVAL, "null tensor argument");
     if (!aligned16(x_bf16) || !aligned16(prepared)) return fail(NARHIP_EINVAL, "x and prepared must be 16-byte aligned");

@@ -130,7 +130,7 @@ def launch_projection_dot(x: torch.Tensor, y_padded: torch.Tensor, partial: torc
     if partial.shape != (tokens, config.splits * k):
         raise ValueError(f"partial must be [{tokens}, {config.splits * k}]")
     v = _factor_from_terms(y_padded, n, k, terms)
-    if n % (32 * config.splits) == 0:
+    if n % (128 * config.splits) == 0:
         prep = cached_prepared(v, None, n, k)
         return ops.rank_projection(x, v, partial, ops.RANK_MFMA, prepared=prep)
     return ops.rank_projection(x, v, partial, ops.RANK_EXACT)
