@@ -461,12 +461,12 @@ int run_rotate_quant(const void *x_bf16, int64_t T, int64_t n, int64_t ldx, int 
             if (p.kron) {
                 KronArgs ka{};
                 ka.x = xc; ka.ldx = ldx; ka.T = tn; ka.n = n; ka.signs = signs; ka.P = Pbuf;
-                ka.paley = paley_table(m); ka.sq = f32_sqrt(q); ka.hm = 1.0f / f32_sqrt(m);
+                ka.paley = paley_table(m); ka.sq = f32_sqrt(q); ka.rsq = 1.0f / ka.sq; ka.hm = 1.0f / f32_sqrt(m);
                 if ((rc = launch_kron(nullptr, &ka, false, m, q, group, s))) return rc;
             } else {
                 SegArgs sa{};
                 sa.x = xc; sa.ldx = ldx; sa.T = tn; sa.n = n; sa.signs = signs; sa.k = 0;
-                sa.codes = nullptr; sa.rotated = Pbuf; sa.sq = f32_sqrt(q);
+                sa.codes = nullptr; sa.rotated = Pbuf; sa.sq = f32_sqrt(q); sa.rsq = 1.0f / sa.sq;
                 if ((rc = launch_seg(sa, q, group, RANK_NONE, s))) return rc;
             }
             CorrQuantArgs ca{};
@@ -498,7 +498,7 @@ int run_rotate_quant(const void *x_bf16, int64_t T, int64_t n, int64_t ldx, int 
             ka.x = x; ka.ldx = ldx; ka.T = T; ka.n = n; ka.signs = signs;
             ka.codes = codes; ka.scales = static_cast<uint16_t *>(scales); ka.zeros = static_cast<uint16_t *>(zeros);
             ka.dest = dest; ka.rotated = rotated;
-            ka.paley = paley_table(m); ka.sq = f32_sqrt(q); ka.hm = 1.0f / f32_sqrt(m);
+            ka.paley = paley_table(m); ka.sq = f32_sqrt(q); ka.rsq = 1.0f / ka.sq; ka.hm = 1.0f / f32_sqrt(m);
             return launch_kron(nullptr, &ka, true, m, q, group, s);
         }
         RowArgs a{};
@@ -506,14 +506,14 @@ int run_rotate_quant(const void *x_bf16, int64_t T, int64_t n, int64_t ldx, int 
         a.signs = signs; a.corr = k > 0 ? corr : nullptr;
         a.codes = codes; a.scales = static_cast<uint16_t *>(scales); a.zeros = static_cast<uint16_t *>(zeros);
         a.dest = dest; a.rotated = rotated; a.paley = paley_table(m);
-        a.sq = f32_sqrt(q); a.hm = 1.0f / f32_sqrt(m);
+        a.sq = f32_sqrt(q); a.rsq = 1.0f / a.sq; a.hm = 1.0f / f32_sqrt(m);
         return launch_kron(&a, nullptr, true, m, q, group, s);
     }
     SegArgs a{};
     a.x = x; a.ldx = ldx; a.T = T; a.n = n;
     a.signs = signs; a.v = v; a.wt = wt; a.partial = part; a.splits = sp; a.k = k;
     a.codes = codes; a.scales = static_cast<uint16_t *>(scales); a.zeros = static_cast<uint16_t *>(zeros);
-    a.dest = dest; a.rotated = rotated; a.sq = f32_sqrt(q);
+    a.dest = dest; a.rotated = rotated; a.sq = f32_sqrt(q); a.rsq = 1.0f / a.sq;
     return launch_seg(a, q, group, p.seg_mode, s);
 }
 

@@ -141,6 +141,71 @@ __device__ __forceinline__ uint32_t quant_code(float x, const GroupParams &g)
     return (uint32_t)q;
 }
 
+// The same code from y = (x - z) * RN(1/s).  y is within 2^-23 |d/s| of the
+// exact quotient and RN(d/s) within 2^-24 |d/s|, so below 16 both round to the
+// same integer unless y lies within 2^-18 of a half-integer; such lanes set
+// `tie` and the caller recomputes with quant_code.  (Half-integers at or above
+// 15.5 and below 0.5 clamp to the same code either way.)
+__device__ __forceinline__ uint32_t quant_code_fast(float x, float z, float rs, bool &tie)
+{
+    const float y = (x - z) * rs;
+    const float r = __builtin_rintf(y);
+    tie |= __builtin_fabsf(y - r) >= 0.5f - 0x1p-18f;
+    return (uint32_t)fminf(fmaxf(r, 0.0f), 15.0f);
+}
+
+// Eight codes of one lane packed into a 32-bit word (nibble e = element e).
+// Bit-identical to eight quant_code calls; the exact division only runs for
+// waves that hold a near-tie.
+__device__ __forceinline__ uint32_t quant_word8(const float *v, const GroupParams &g)
+{
+    const float rs = 1.0f / g.s;
+    bool tie = false;
+    uint32_t word = 0;
+#pragma unroll
+    for (int e = 0; e < 8; e++) word |= quant_code_fast(v[e], g.z, rs, tie) << (4 * e);
+    if (__builtin_expect(__any(tie), 0)) {
+        word = 0;
+#pragma unroll
+        for (int e = 0; e < 8; e++) word |= quant_code(v[e], g) << (4 * e);
+    }
+    return word;
+}
+
+// ------------------------------------------------- division by fp32(sqrt Q) --
+//
+// v[i] <- RN(v[i] / c) with c = fp32(sqrt(Q)), rc = RN(1/c).
+// Q a power of 4: c is a power of two and RN(v * rc) is the quotient.
+// Otherwise q0 = v*rc, r = fma(q0, c, -v), q1 = fma(-r, rc, q0), which was
+// checked against the correctly rounded fp32 quotient for every finite fp32 v
+// of both signs and Q in {2, 8, 12, 28, 32, 128, 512, 2048}: equal for all
+// |v| >= 2^-100.  A wave holding any |v| < 2^-100 (zeros included) takes the
+// division instead.
+template <int Q, int NV>
+__device__ __forceinline__ void div_sqrt_q(float (&v)[NV], float c, float rc)
+{
+    constexpr bool pow4 = (Q & (Q - 1)) == 0 && (Q & 0x55555555) == Q;
+    if constexpr (pow4) {
+#pragma unroll
+        for (int i = 0; i < NV; i++) v[i] *= rc;
+    } else {
+        bool tiny = false;
+#pragma unroll
+        for (int i = 0; i < NV; i++) tiny |= __builtin_fabsf(v[i]) < 0x1p-100f;
+        if (__builtin_expect(__any(tiny), 0)) {
+#pragma unroll
+            for (int i = 0; i < NV; i++) v[i] = v[i] / c;
+        } else {
+#pragma unroll
+            for (int i = 0; i < NV; i++) {
+                const float q0 = v[i] * rc;
+                const float r = __builtin_fmaf(q0, c, -v[i]);
+                v[i] = __builtin_fmaf(-r, rc, q0);
+            }
+        }
+    }
+}
+
 // ----------------------------------------------------------------- Paley --
 
 // Rows of the +-1 Paley matrices as bit masks: bit a' of row a set <=> entry -1.

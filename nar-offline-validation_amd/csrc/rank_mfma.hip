@@ -244,13 +244,26 @@ corr_quant_kernel(CorrQuantArgs a)
             lo = fminf(lo, __shfl_xor(lo, 16)); hi = fmaxf(hi, __shfl_xor(hi, 16));
             lo = fminf(lo, __shfl_xor(lo, 32)); hi = fmaxf(hi, __shfl_xor(hi, 32));
             const GroupParams gp = group_params(lo, hi);
+            const float rs = 1.0f / gp.s;
+            bool tie = false;
+            uint32_t q4[MTG];
 #pragma unroll
             for (int j = 0; j < MTG; j++) {
-                uint32_t q4 = 0;
+                q4[j] = 0;
 #pragma unroll
-                for (int i = 0; i < 4; i++) q4 |= quant_code(xv[gq * MTG + j][i], gp) << (8 * i);
-                *reinterpret_cast<uint32_t *>(&cstage[tl][16 * (gq * MTG + j) + 4 * g]) = q4;
+                for (int i = 0; i < 4; i++) q4[j] |= quant_code_fast(xv[gq * MTG + j][i], gp.z, rs, tie) << (8 * i);
             }
+            if (__builtin_expect(__any(tie), 0)) {
+#pragma unroll
+                for (int j = 0; j < MTG; j++) {
+                    q4[j] = 0;
+#pragma unroll
+                    for (int i = 0; i < 4; i++) q4[j] |= quant_code(xv[gq * MTG + j][i], gp) << (8 * i);
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < MTG; j++)
+                *reinterpret_cast<uint32_t *>(&cstage[tl][16 * (gq * MTG + j) + 4 * g]) = q4[j];
             if (g == 0 && tok_ok) {
                 const int64_t gi = orow * (a.n / B) + (c0 + gq * B) / B;
                 a.scales[gi] = gp.s16;

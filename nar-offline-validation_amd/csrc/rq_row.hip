@@ -26,7 +26,7 @@ struct RowArgs {
     const int64_t *dest;
     float *rotated;
     PaleyTable paley;
-    float sq;               // fp32(sqrt(Q))
+    float sq, rsq;          // fp32(sqrt(Q)), RN(1/sq)
     float hm;               // fp32(1) / fp32(sqrt(M))
 };
 
@@ -98,12 +98,12 @@ rq_row_kernel(RowArgs a)
                         v[h * 8 + e] = x0 + x1;
                         v[(h + wh) * 8 + e] = x0 - x1;
                     }
-        const float sq = a.sq;
+        div_sqrt_q<Q>(v, a.sq, a.rsq);
 #pragma unroll
         for (int h = 0; h < NH; h++) {
             float4 *d = reinterpret_cast<float4 *>(F + s * Q + h * 128 + chunk * 8);
-            d[0] = make_float4(v[h * 8 + 0] / sq, v[h * 8 + 1] / sq, v[h * 8 + 2] / sq, v[h * 8 + 3] / sq);
-            d[1] = make_float4(v[h * 8 + 4] / sq, v[h * 8 + 5] / sq, v[h * 8 + 6] / sq, v[h * 8 + 7] / sq);
+            d[0] = make_float4(v[h * 8 + 0], v[h * 8 + 1], v[h * 8 + 2], v[h * 8 + 3]);
+            d[1] = make_float4(v[h * 8 + 4], v[h * 8 + 5], v[h * 8 + 6], v[h * 8 + 7]);
         }
     }
     __syncthreads();
@@ -158,9 +158,7 @@ rq_row_kernel(RowArgs a)
         for (int e = 1; e < 8; e++) { lo = fminf(lo, v[e]); hi = fmaxf(hi, v[e]); }
         group_minmax<G8>(lo, hi);
         const GroupParams g = group_params(lo, hi);
-        uint32_t word = 0;
-#pragma unroll
-        for (int e = 0; e < 8; e++) word |= quant_code(v[e], g) << (4 * e);
+        const uint32_t word = quant_word8(v, g);
         if (ok) {
             *reinterpret_cast<uint32_t *>(a.codes + orow * (N / 2) + ch * 4) = word;
             if ((ch % G8) == 0) {

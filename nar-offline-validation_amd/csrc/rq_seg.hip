@@ -31,7 +31,7 @@ struct SegArgs {
     uint16_t *zeros;
     const int64_t *dest;    // [T] output row per token, or null
     float *rotated;         // [T, n] or null
-    float sq;               // fp32(sqrt(Q)), computed on the host
+    float sq, rsq;          // fp32(sqrt(Q)) and RN(1/sq), computed on the host
 };
 
 template <int Q, int B, int MODE, int KMAX>
@@ -144,11 +144,7 @@ rq_seg_kernel(SegArgs a)
                     v[(h + wh) * 8 + e] = x0 - x1;
                 }
     // normalisation: fp32 division by fp32(sqrt(Q))
-    {
-        const float sq = a.sq;
-#pragma unroll
-        for (int i = 0; i < NV; i++) v[i] = v[i] / sq;
-    }
+    div_sqrt_q<Q>(v, a.sq, a.rsq);
 
     // ---- rank-k correction: x' = Hx - RN32(sum_r u_r W[r, i])
     if constexpr (MODE != RANK_NONE) {
@@ -186,9 +182,7 @@ rq_seg_kernel(SegArgs a)
         for (int e = 1; e < 8; e++) { lo = fminf(lo, v[h * 8 + e]); hi = fmaxf(hi, v[h * 8 + e]); }
         group_minmax<G8>(lo, hi);
         const GroupParams g = group_params(lo, hi);
-        uint32_t word = 0;
-#pragma unroll
-        for (int e = 0; e < 8; e++) word |= quant_code(v[h * 8 + e], g) << (4 * e);
+        const uint32_t word = quant_word8(v + h * 8, g);
         if (active) {
             const int64_t pos = base + h * 128 + chunk * 8;
             *reinterpret_cast<uint32_t *>(a.codes + orow * (a.n / 2) + pos / 2) = word;
