@@ -43,7 +43,31 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--rank-mode", default="auto", choices=["auto", "exact", "mfma"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU baseline work")
+    ap.add_argument("--copy-mb", type=int, default=0,
+                    help="instead of the workload, time a plain device copy of this many MiB (the "
+                         "reference reading for the FETCH_SIZE / WRITE_SIZE byte counters)")
     return ap.parse_args()
+
+
+def copy_calibration(mib: int, steps: int) -> int:
+    import torch
+    dev = torch.device("cuda:0")
+    nbytes = mib << 20
+    src = torch.empty(nbytes // 4, dtype=torch.float32, device=dev).uniform_()
+    dst = torch.empty_like(src)
+    for _ in range(2):
+        dst.copy_(src)
+    torch.cuda.synchronize(dev)
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for _ in range(steps):
+        dst.copy_(src)
+    ev1.record()
+    torch.cuda.synchronize(dev)
+    ms = ev0.elapsed_time(ev1) / steps
+    print(json.dumps({"copy_bytes_read": nbytes, "copy_bytes_written": nbytes, "ms_per_copy": ms,
+                      "gbps": 2 * nbytes / (ms * 1e-3) / 1e9}), flush=True)
+    return 0
 
 
 def describe(w) -> str:
@@ -95,6 +119,9 @@ def main() -> int:
               "shards by tokens with no communication (see DESIGN.md); run with --gpus 1.",
               file=sys.stderr)
         return 2
+
+    if args.copy_mb:
+        return copy_calibration(args.copy_mb, args.steps)
 
     import numpy as np
     import torch

@@ -296,6 +296,15 @@ int launch_proj_mfma(const uint16_t *x, int64_t T, int64_t n, int64_t ldx, const
     return check_launch("proj_mfma_kernel");
 }
 
+int launch_fold_u(const float *partial, int splits, int k, int kp, int64_t T, __bf16 *u3, hipStream_t s)
+{
+    const int64_t n = T * kp;
+    hipLaunchKernelGGL(fold_u_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, partial, splits, k, kp, T, u3);
+    return check_launch("fold_u_kernel");
+}
+
+size_t u3_bytes(int64_t T, int k) { return sizeof(uint16_t) * 3 * (size_t)kp32(k) * (size_t)T; }
+
 template <int B>
 int launch_cq_b(const CorrQuantArgs &a, int ks, dim3 grid, hipStream_t s)
 {
@@ -304,14 +313,27 @@ int launch_cq_b(const CorrQuantArgs &a, int ks, dim3 grid, hipStream_t s)
     return check_launch("corr_quant_kernel");
 }
 
+// Channels per workgroup: the widest power-of-two multiple of the group that
+// divides n and still gives >= 1024 workgroups (128 tokens each); the group
+// itself when none does.
+int64_t corr_channels(int64_t T, int64_t n, int b)
+{
+    const int64_t tblocks = (T + 127) / 128;
+    int64_t best = b;
+    for (int64_t cw = b; cw <= n; cw *= 2)
+        if (n % cw == 0 && tblocks * (n / cw) >= 1024) best = cw;
+    return best;
+}
+
 int launch_corr_quant(CorrQuantArgs a, int b, hipStream_t s)
 {
     if (a.T == 0) return NARHIP_OK;
-    int64_t cw = 1024;
-    while (cw > 128 && a.n % cw) cw /= 2;
-    if (a.n % cw) return fail(NARHIP_EUNSUPPORTED, "rank correction needs n %% 128 == 0");
-    a.cw = cw;
-    dim3 grid((unsigned)((a.T + 63) / 64), (unsigned)(a.n / cw));
+    if (a.n % b) return fail(NARHIP_EUNSUPPORTED, "rank correction needs n %% group == 0");
+    a.cw = corr_channels(a.T, a.n, b);
+    a.ncb = a.n / a.cw;
+    const int64_t blocks = (a.T + 127) / 128 * a.ncb;
+    if (blocks > 0x7fffffff) return fail(NARHIP_EUNSUPPORTED, "too many tokens");
+    dim3 grid((unsigned)blocks);
     const int ks = a.kp / 32;
     switch (b) {
     case 32: return launch_cq_b<32>(a, ks, grid, s);
@@ -350,8 +372,11 @@ struct Plan {
     bool need_prep, need_proj, need_P, need_corr;
     int splits;
     int64_t chunk;
-    size_t prep_b, proj_b, P_b, corr_b;
-    size_t total() const { return align256(prep_b) + align256(proj_b) + align256(P_b) + align256(corr_b); }
+    size_t prep_b, proj_b, P_b, corr_b, u_b;
+    size_t total() const
+    {
+        return align256(prep_b) + align256(proj_b) + align256(P_b) + align256(corr_b) + align256(u_b);
+    }
 };
 
 int make_plan(int64_t T, int64_t n, int m, int q, int k, int64_t nb, bool have_partial, int splits,
@@ -397,6 +422,7 @@ int make_plan(int64_t T, int64_t n, int m, int q, int k, int64_t nb, bool have_p
         p.proj_b = p.need_proj ? sizeof(float) * (size_t)p.chunk * (size_t)p.splits * (size_t)k : 0;
         p.need_P = true;
         p.P_b = sizeof(float) * (size_t)p.chunk * (size_t)n;
+        p.u_b = u3_bytes(p.chunk, k);
         return NARHIP_OK;
     }
     p.need_proj = !have_partial;
@@ -444,6 +470,8 @@ int run_rotate_quant(const void *x_bf16, int64_t T, int64_t n, int64_t ldx, int 
     float *Pbuf = p.need_P ? reinterpret_cast<float *>(wsp) : nullptr;
     wsp += align256(p.P_b);
     float *corr = p.need_corr ? reinterpret_cast<float *>(wsp) : nullptr;
+    wsp += align256(p.corr_b);
+    __bf16 *u3 = p.u_b ? reinterpret_cast<__bf16 *>(wsp) : nullptr;
     const uint16_t *x = static_cast<const uint16_t *>(x_bf16);
 
     if (p.path == PATH_MFMA_RANK) {
@@ -469,8 +497,9 @@ int run_rotate_quant(const void *x_bf16, int64_t T, int64_t n, int64_t ldx, int 
                 sa.codes = nullptr; sa.rotated = Pbuf; sa.sq = f32_sqrt(q); sa.rsq = 1.0f / sa.sq;
                 if ((rc = launch_seg(sa, q, group, RANK_NONE, s))) return rc;
             }
+            if ((rc = launch_fold_u(part, sp, k, kp32(k), tn, u3, s))) return rc;
             CorrQuantArgs ca{};
-            ca.P = Pbuf; ca.T = tn; ca.n = n; ca.partial = part; ca.splits = sp; ca.k = k;
+            ca.P = Pbuf; ca.T = tn; ca.n = n; ca.u3 = u3;
             ca.wtt = reinterpret_cast<const __bf16 *>(static_cast<const char *>(prep) + vt_bytes(n, k));
             ca.kp = kp32(k);
             ca.dest = dest ? dest + t0 : nullptr;

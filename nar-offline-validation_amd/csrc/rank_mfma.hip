@@ -7,10 +7,11 @@
 //                     (nar/kernels/r4_fused_v3.py:83-135): x is bf16 (exact),
 //                     V enters as hi/mid/lo terms, hi and mid+lo in separate
 //                     accumulators, folded in fp64 at the end of the split
+//   fold_u          : u = fp64 fold of the split partials, rounded once, as
+//                     three bf16 terms per token
 //   corr_quant      : x' = P - u W^T with u and W^T both as three bf16 terms
 //                     (the six term products of weight >= 2^-16), then the
 //                     INT4 quantizer of nar/experiment.py:158-184
-// Factor tiles are staged in LDS once per workgroup and shared by its waves.
 #include "mfma.hpp"
 #include "narhip_device.hpp"
 
@@ -133,160 +134,190 @@ proj_mfma_kernel(ProjMfmaArgs a)
     }
 }
 
+// u for each token from the split partials: fp64 fold in split order, rounded
+// once to fp32, then split in three bf16 terms.  u3 [T][3][kp] (zero for r >= k).
+__global__ void __launch_bounds__(256)
+fold_u_kernel(const float *partial, int splits, int k, int kp, int64_t T, __bf16 *u3)
+{
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= T * kp) return;
+    const int64_t t = idx / kp;
+    const int r = (int)(idx % kp);
+    double sum = 0.0;
+    if (r < k) {
+        const float *pp = partial + t * (int64_t)splits * k + r;
+        for (int s = 0; s < splits; s++) sum += (double)pp[(int64_t)s * k];
+    }
+    __bf16 h, m, l;
+    split3((float)sum, h, m, l);
+    __bf16 *o = u3 + t * 3 * kp + r;
+    o[0] = h; o[kp] = m; o[2 * kp] = l;
+}
+
 struct CorrQuantArgs {
     const float *P;        // [T, n] rotated rows before the rank term
     int64_t T, n;
-    const float *partial;  // [T, splits*k]
-    int splits, k;
-    const __bf16 *wtt;     // [3][n][kp]
+    const __bf16 *u3;      // [T][3][kp] terms of u
+    const __bf16 *wtt;     // [3][n][kp] terms of W^T
     int kp;
     uint8_t *codes;
     uint16_t *scales;
     uint16_t *zeros;
     const int64_t *dest;
     float *rotated;        // optional x' [T, n]
-    int64_t cw;            // channels per workgroup (multiple of 128)
+    int64_t cw;            // channels per workgroup (multiple of the group)
+    int64_t ncb;           // n / cw
 };
 
-// grid (ceil(T/64), n/cw), block 256.  Tile: 64 tokens (wave w: tokens 16w..16w+15,
-// the MFMA N dimension) x 128-channel sub-tiles (8 M tiles of 16 channels).
-// Lane l holds x' for token 16w + l%16 and channels 16 mt + 4g .. +3 (g = l/16).
+// grid ((T/128) * ncb), block 256.  Every wave works alone (no workgroup
+// barriers): 32 tokens (two MFMA N tiles) x the cw channels of the block, one
+// quantization group of B channels (B/16 M tiles) at a time.  Lane l holds
+// x' for tokens 16 nt + l%16 and channels 16 mt + 4g .. +3 (g = l/16).  The
+// P tile of a group is loaded before its MFMAs; W^T fragments come straight
+// from L2.  Blocks with consecutive ids take different channel blocks, so
+// each XCD keeps only its share of W^T in its L2.
 template <int B, int KS>
 __global__ void __launch_bounds__(256)
 corr_quant_kernel(CorrQuantArgs a)
 {
     constexpr int KP = 32 * KS;
-    __shared__ __bf16 us[3][64][KP + 8];
-    __shared__ __bf16 ws[3][128][KP + 8];
-    __shared__ uint8_t cstage[64][128 + 16];
+    constexpr int MTG = B / 16;            // M tiles per group
+    constexpr int NT = 2;                  // 16-token N tiles per wave
+    constexpr int RW = B / 4 + 4;          // uint16 slots per token row of the code stage (8-byte rows)
+    __shared__ __align__(16) uint16_t cst[4][16 * NT][RW];
     const int tid = threadIdx.x;
     const int lane = tid & 63, w = tid >> 6;
     const int g = lane >> 4, c16 = lane & 15;
-    const int64_t t0 = (int64_t)blockIdx.x * 64;
-    const int64_t cbase = (int64_t)blockIdx.y * a.cw;
-    const int tl = 16 * w + c16;                 // this lane's token within the tile
-    const int64_t t = t0 + tl;
-    const int64_t tc = t < a.T ? t : a.T - 1;
-    const bool tok_ok = t < a.T;
+    const int64_t cb = (int64_t)blockIdx.x % a.ncb;
+    const int64_t tb = (int64_t)blockIdx.x / a.ncb;
+    const int64_t t0 = tb * 128 + w * 32;
+    if (t0 >= a.T) return;
+    const int64_t plane = (int64_t)KP * a.n;
+    const int64_t gpt = a.n / B;
 
-    // u for the 64 tokens: fp64 fold of the split partials, rounded once, split in 3
-    for (int p = tid; p < 64 * KP; p += 256) {
-        const int tt = p / KP, r = p % KP;
-        const int64_t tg = t0 + tt;
-        double sum = 0.0;
-        if (tg < a.T && r < a.k) {
-            const float *pp = a.partial + tg * (int64_t)a.splits * a.k + r;
-            for (int s = 0; s < a.splits; s++) sum += (double)pp[(int64_t)s * a.k];
-        }
-        __bf16 h, m, l;
-        split3((float)sum, h, m, l);
-        us[0][tt][r] = h; us[1][tt][r] = m; us[2][tt][r] = l;
+    int64_t tok[NT], orow[NT];
+    bf16x8 ub[3][NT][KS];
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++) {
+        const int64_t t = t0 + 16 * nt + c16;
+        tok[nt] = t < a.T ? t : a.T - 1;
+        orow[nt] = t < a.T ? (a.dest ? a.dest[t] : t) : -1;
+#pragma unroll
+        for (int term = 0; term < 3; term++)
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++)
+                ub[term][nt][ks] = load_bf16x8(a.u3 + (tok[nt] * 3 + term) * KP + 32 * ks + 8 * g);
     }
-    __syncthreads();
-    bf16x8 ub[3][KS];
-#pragma unroll
-    for (int term = 0; term < 3; term++)
-#pragma unroll
-        for (int ks = 0; ks < KS; ks++)
-            ub[term][ks] = *reinterpret_cast<const bf16x8 *>(&us[term][tl][32 * ks + 8 * g]);
 
-    const int64_t plane = (int64_t)a.kp * a.n;
-    const int64_t orow = tok_ok ? (a.dest ? a.dest[t] : t) : 0;
-    for (int64_t c0 = cbase; c0 < cbase + a.cw; c0 += 128) {
-        // stage W^T terms of these 128 channels
-        for (int p = tid; p < 3 * 128 * (KP / 8); p += 256) {
-            const int term = p / (128 * (KP / 8));
-            const int rem = p % (128 * (KP / 8));
-            const int ch = rem / (KP / 8), r8 = rem % (KP / 8);
-            *reinterpret_cast<bf16x8 *>(&ws[term][ch][r8 * 8]) =
-                load_bf16x8(a.wtt + term * plane + (c0 + ch) * a.kp + r8 * 8);
-        }
-        __syncthreads();
-        float xv[8][4];
-        const float *prow = a.P + tc * a.n + c0 + 4 * g;
+    for (int64_t c0 = cb * a.cw; c0 < (cb + 1) * a.cw; c0 += B) {
+        float xv[MTG][NT][4];
 #pragma unroll
-        for (int mt = 0; mt < 8; mt++) {
-            const float4 pv = *reinterpret_cast<const float4 *>(prow + 16 * mt);
-            floatx4 main = zero4(), small = zero4();
+        for (int mt = 0; mt < MTG; mt++)
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) {
+                const float4 pv = *reinterpret_cast<const float4 *>(a.P + tok[nt] * a.n + c0 + 16 * mt + 4 * g);
+                xv[mt][nt][0] = pv.x; xv[mt][nt][1] = pv.y; xv[mt][nt][2] = pv.z; xv[mt][nt][3] = pv.w;
+            }
+#pragma unroll
+        for (int mt = 0; mt < MTG; mt++) {
+            const __bf16 *wrow = a.wtt + (c0 + 16 * mt + c16) * KP + 8 * g;
+            bf16x8 wh[KS], wm[KS], wl[KS];
 #pragma unroll
             for (int ks = 0; ks < KS; ks++) {
-                const bf16x8 wh = *reinterpret_cast<const bf16x8 *>(&ws[0][16 * mt + c16][32 * ks + 8 * g]);
-                const bf16x8 wm = *reinterpret_cast<const bf16x8 *>(&ws[1][16 * mt + c16][32 * ks + 8 * g]);
-                const bf16x8 wl = *reinterpret_cast<const bf16x8 *>(&ws[2][16 * mt + c16][32 * ks + 8 * g]);
-                main = mfma_bf16(wh, ub[0][ks], main);
-                small = mfma_bf16(wm, ub[0][ks], small);
-                small = mfma_bf16(wh, ub[1][ks], small);
-                small = mfma_bf16(wl, ub[0][ks], small);
-                small = mfma_bf16(wh, ub[2][ks], small);
-                small = mfma_bf16(wm, ub[1][ks], small);
+                wh[ks] = load_bf16x8(wrow + 32 * ks);
+                wm[ks] = load_bf16x8(wrow + plane + 32 * ks);
+                wl[ks] = load_bf16x8(wrow + 2 * plane + 32 * ks);
             }
-            xv[mt][0] = pv.x - (main[0] + small[0]);
-            xv[mt][1] = pv.y - (main[1] + small[1]);
-            xv[mt][2] = pv.z - (main[2] + small[2]);
-            xv[mt][3] = pv.w - (main[3] + small[3]);
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) {
+                floatx4 main = zero4(), small = zero4();
+#pragma unroll
+                for (int ks = 0; ks < KS; ks++) {
+                    main = mfma_bf16(wh[ks], ub[0][nt][ks], main);
+                    small = mfma_bf16(wm[ks], ub[0][nt][ks], small);
+                    small = mfma_bf16(wh[ks], ub[1][nt][ks], small);
+                    small = mfma_bf16(wl[ks], ub[0][nt][ks], small);
+                    small = mfma_bf16(wh[ks], ub[2][nt][ks], small);
+                    small = mfma_bf16(wm[ks], ub[1][nt][ks], small);
+                }
+#pragma unroll
+                for (int i = 0; i < 4; i++) xv[mt][nt][i] = xv[mt][nt][i] - (main[i] + small[i]);
+            }
         }
-        if (a.rotated && tok_ok) {
+        if (a.rotated) {
 #pragma unroll
-            for (int mt = 0; mt < 8; mt++)
-                *reinterpret_cast<float4 *>(a.rotated + t * a.n + c0 + 16 * mt + 4 * g) =
-                    make_float4(xv[mt][0], xv[mt][1], xv[mt][2], xv[mt][3]);
+            for (int nt = 0; nt < NT; nt++)
+                if (orow[nt] >= 0)
+#pragma unroll
+                    for (int mt = 0; mt < MTG; mt++)
+                        *reinterpret_cast<float4 *>(a.rotated + tok[nt] * a.n + c0 + 16 * mt + 4 * g) =
+                            make_float4(xv[mt][nt][0], xv[mt][nt][1], xv[mt][nt][2], xv[mt][nt][3]);
         }
-        // quantize: a group of B channels = B/16 M tiles x the four lane groups g
-        // (lanes c16, c16+16, c16+32, c16+48 hold the same token)
-        constexpr int MTG = B / 16;
+        // quantize: the group of token (nt, c16) is spread over lanes c16 + 16g
 #pragma unroll
-        for (int gq = 0; gq < 8 / MTG; gq++) {
-            float lo = xv[gq * MTG][0], hi = lo;
+        for (int nt = 0; nt < NT; nt++) {
+            float lo = xv[0][nt][0], hi = lo;
 #pragma unroll
-            for (int j = 0; j < MTG; j++)
+            for (int mt = 0; mt < MTG; mt++)
 #pragma unroll
-                for (int i = 0; i < 4; i++) { lo = fminf(lo, xv[gq * MTG + j][i]); hi = fmaxf(hi, xv[gq * MTG + j][i]); }
+                for (int i = 0; i < 4; i++) { lo = fminf(lo, xv[mt][nt][i]); hi = fmaxf(hi, xv[mt][nt][i]); }
             lo = fminf(lo, __shfl_xor(lo, 16)); hi = fmaxf(hi, __shfl_xor(hi, 16));
             lo = fminf(lo, __shfl_xor(lo, 32)); hi = fmaxf(hi, __shfl_xor(hi, 32));
             const GroupParams gp = group_params(lo, hi);
             const float rs = 1.0f / gp.s;
             bool tie = false;
-            uint32_t q4[MTG];
+            uint32_t q16[MTG];
 #pragma unroll
-            for (int j = 0; j < MTG; j++) {
-                q4[j] = 0;
+            for (int mt = 0; mt < MTG; mt++) {
+                q16[mt] = 0;
 #pragma unroll
-                for (int i = 0; i < 4; i++) q4[j] |= quant_code_fast(xv[gq * MTG + j][i], gp.z, rs, tie) << (8 * i);
+                for (int i = 0; i < 4; i++) q16[mt] |= quant_code_fast(xv[mt][nt][i], gp.z, rs, tie) << (4 * i);
             }
             if (__builtin_expect(__any(tie), 0)) {
 #pragma unroll
-                for (int j = 0; j < MTG; j++) {
-                    q4[j] = 0;
+                for (int mt = 0; mt < MTG; mt++) {
+                    q16[mt] = 0;
 #pragma unroll
-                    for (int i = 0; i < 4; i++) q4[j] |= quant_code(xv[gq * MTG + j][i], gp) << (8 * i);
+                    for (int i = 0; i < 4; i++) q16[mt] |= quant_code(xv[mt][nt][i], gp) << (4 * i);
                 }
             }
 #pragma unroll
-            for (int j = 0; j < MTG; j++)
-                *reinterpret_cast<uint32_t *>(&cstage[tl][16 * (gq * MTG + j) + 4 * g]) = q4[j];
-            if (g == 0 && tok_ok) {
-                const int64_t gi = orow * (a.n / B) + (c0 + gq * B) / B;
+            for (int mt = 0; mt < MTG; mt++) cst[w][16 * nt + c16][4 * mt + g] = (uint16_t)q16[mt];
+            if (g == 0 && orow[nt] >= 0) {
+                const int64_t gi = orow[nt] * gpt + c0 / B;
                 a.scales[gi] = gp.s16;
                 a.zeros[gi] = gp.z16;
             }
         }
-        __syncthreads();
-        // pack: 64 tokens x 16 words (8 codes each), 4 per thread
-#pragma unroll
-        for (int p = 0; p < 4; p++) {
-            const int idx = tid + 256 * p;
-            const int tt = idx >> 4, wd = idx & 15;
-            const int64_t tg = t0 + tt;
-            const uint8_t *src = &cstage[tt][wd * 8];
-            uint32_t word = 0;
-#pragma unroll
-            for (int e = 0; e < 8; e++) word |= (uint32_t)src[e] << (4 * e);
-            if (tg < a.T) {
-                const int64_t orw = a.dest ? a.dest[tg] : tg;
-                *reinterpret_cast<uint32_t *>(a.codes + orw * (a.n / 2) + (c0 + wd * 8) / 2) = word;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        // store: two lanes per token, B/4 bytes each
+        {
+            const int tl = lane >> 1, half = lane & 1;
+            const int64_t t = t0 + tl;
+            const uint16_t *src = &cst[w][tl][half * (B / 8)];
+            if (t < a.T) {
+                const int64_t r = a.dest ? a.dest[t] : t;
+                uint8_t *dst = a.codes + r * (a.n / 2) + c0 / 2 + half * (B / 4);
+                if constexpr (B == 128) {
+                    const uint2 *s2 = reinterpret_cast<const uint2 *>(src);
+                    uint4 v0 = make_uint4(s2[0].x, s2[0].y, s2[1].x, s2[1].y);
+                    uint4 v1 = make_uint4(s2[2].x, s2[2].y, s2[3].x, s2[3].y);
+                    reinterpret_cast<uint4 *>(dst)[0] = v0;
+                    reinterpret_cast<uint4 *>(dst)[1] = v1;
+                } else if constexpr (B == 64) {
+                    const uint2 *s2 = reinterpret_cast<const uint2 *>(src);
+                    reinterpret_cast<uint4 *>(dst)[0] = make_uint4(s2[0].x, s2[0].y, s2[1].x, s2[1].y);
+                } else {
+                    const uint2 *s2 = reinterpret_cast<const uint2 *>(src);
+                    reinterpret_cast<uint2 *>(dst)[0] = s2[0];
+                }
             }
         }
-        __syncthreads();
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
 }
 
