@@ -305,40 +305,46 @@ int launch_fold_u(const float *partial, int splits, int k, int kp, int64_t T, __
 
 size_t u3_bytes(int64_t T, int k) { return sizeof(uint16_t) * 3 * (size_t)kp32(k) * (size_t)T; }
 
-template <int B>
-int launch_cq_b(const CorrQuantArgs &a, int ks, dim3 grid, hipStream_t s)
+template <int B, int KS, int CW>
+int launch_cq(const CorrQuantArgs &a, dim3 grid, hipStream_t s)
 {
-    if (ks == 1) hipLaunchKernelGGL((corr_quant_kernel<B, 1>), grid, dim3(256), 0, s, a);
-    else hipLaunchKernelGGL((corr_quant_kernel<B, 2>), grid, dim3(256), 0, s, a);
+    hipLaunchKernelGGL((corr_quant_kernel<B, KS, CW>), grid, dim3(256), 0, s, a);
     return check_launch("corr_quant_kernel");
 }
 
-// Channels per workgroup: the widest power-of-two multiple of the group that
-// divides n and still gives >= 1024 workgroups (128 tokens each); the group
-// itself when none does.
-int64_t corr_channels(int64_t T, int64_t n, int b)
+#ifndef NARHIP_CQ_CW_K32
+#define NARHIP_CQ_CW_K32 256
+#endif
+
+template <int B>
+int launch_cq_b(const CorrQuantArgs &a, int ks, int cw, dim3 grid, hipStream_t s)
 {
-    const int64_t tblocks = (T + 127) / 128;
-    int64_t best = b;
-    for (int64_t cw = b; cw <= n; cw *= 2)
-        if (n % cw == 0 && tblocks * (n / cw) >= 1024) best = cw;
-    return best;
+    if (ks == 1 && cw == 256) return launch_cq<B, 1, 256>(a, grid, s);
+    if (ks == 1) return launch_cq<B, 1, 128>(a, grid, s);
+    return launch_cq<B, 2, 128>(a, grid, s);
 }
 
+// Workgroups own 48 KB of W^T terms (256 channels at k <= 32, else 128) and
+// run enough 128-token tiles over them that about 1024 workgroups remain.
 int launch_corr_quant(CorrQuantArgs a, int b, hipStream_t s)
 {
     if (a.T == 0) return NARHIP_OK;
-    if (a.n % b) return fail(NARHIP_EUNSUPPORTED, "rank correction needs n %% group == 0");
-    a.cw = corr_channels(a.T, a.n, b);
-    a.ncb = a.n / a.cw;
-    const int64_t blocks = (a.T + 127) / 128 * a.ncb;
+    const int ks = a.kp / 32;
+    const int cw = (ks == 1 && a.n % 256 == 0) ? NARHIP_CQ_CW_K32 : 128;
+    if (a.n % cw || cw % b) return fail(NARHIP_EUNSUPPORTED, "rank correction needs n %% 128 == 0");
+    a.ncb = a.n / cw;
+    const int64_t tiles = (a.T + 127) / 128;
+    int tpw = 1;
+    while (tpw < 8 && a.ncb * ((tiles + 2 * tpw - 1) / (2 * tpw)) >= 1024) tpw *= 2;
+    a.tpw = tpw;
+    const int64_t groups = (tiles + tpw - 1) / tpw;
+    const int64_t blocks = 8 * a.ncb * ((groups + 7) / 8);
     if (blocks > 0x7fffffff) return fail(NARHIP_EUNSUPPORTED, "too many tokens");
     dim3 grid((unsigned)blocks);
-    const int ks = a.kp / 32;
     switch (b) {
-    case 32: return launch_cq_b<32>(a, ks, grid, s);
-    case 64: return launch_cq_b<64>(a, ks, grid, s);
-    case 128: return launch_cq_b<128>(a, ks, grid, s);
+    case 32: return launch_cq_b<32>(a, ks, cw, grid, s);
+    case 64: return launch_cq_b<64>(a, ks, cw, grid, s);
+    case 128: return launch_cq_b<128>(a, ks, cw, grid, s);
     }
     return fail(NARHIP_EUNSUPPORTED, "group %d not built", b);
 }

@@ -165,159 +165,193 @@ struct CorrQuantArgs {
     uint16_t *zeros;
     const int64_t *dest;
     float *rotated;        // optional x' [T, n]
-    int64_t cw;            // channels per workgroup (multiple of the group)
-    int64_t ncb;           // n / cw
+    int64_t ncb;           // n / CW channel blocks
+    int tpw;               // 128-token tiles per workgroup
 };
 
-// grid ((T/128) * ncb), block 256.  Every wave works alone (no workgroup
-// barriers): 32 tokens (two MFMA N tiles) x the cw channels of the block, one
-// quantization group of B channels (B/16 M tiles) at a time.  Lane l holds
-// x' for tokens 16 nt + l%16 and channels 16 mt + 4g .. +3 (g = l/16).  The
-// P tile of a group is loaded before its MFMAs; W^T fragments come straight
-// from L2.  Blocks with consecutive ids take different channel blocks, so
-// each XCD keeps only its share of W^T in its L2.
-template <int B, int KS>
-__global__ void __launch_bounds__(256)
+// One unit of corr_quant work: 16 tokens (one MFMA N tile) x one quantization
+// group of B channels (B/16 M tiles).  Lane l holds P / x' for token l%16 of
+// the tile and channels 16 mt + 4g .. +3 (g = l/16): B/16 float4 per lane.
+template <int B>
+struct CqUnit {
+    float v[B / 16][4];
+};
+
+template <int B>
+__device__ __forceinline__ void cq_load(CqUnit<B> &p, const float *prow)
+{
+#pragma unroll
+    for (int mt = 0; mt < B / 16; mt++) {
+        const float4 pv = *reinterpret_cast<const float4 *>(prow + 16 * mt);
+        p.v[mt][0] = pv.x; p.v[mt][1] = pv.y; p.v[mt][2] = pv.z; p.v[mt][3] = pv.w;
+    }
+}
+
+// x' = P - u W^T for one unit (W^T terms of the group at wl in LDS, planes of
+// WPLANE elements), then its codes (staged through the wave's LDS rows cst),
+// scales and zeros.  srow: output row of token lane/4 for the code store.
+template <int B, int KS, int WPLANE>
+__device__ __forceinline__ void cq_unit(CqUnit<B> &xt, const CorrQuantArgs &a, const bf16x8 (&ub)[3][KS],
+                                        int64_t tok, int64_t orow, int64_t srow, int64_t c0,
+                                        const __bf16 *wl, uint16_t (*cst)[B / 4 + 4], int lane)
+{
+    constexpr int KP = 32 * KS;
+    constexpr int MTG = B / 16;
+    const int g = lane >> 4, c16 = lane & 15;
+    auto &xv = xt.v;
+#pragma unroll
+    for (int mt = 0; mt < MTG; mt++) {
+        const __bf16 *wrow = wl + (16 * mt + c16) * KP + 8 * g;
+        floatx4 main = zero4(), small = zero4();
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++) {
+            const bf16x8 wh = *reinterpret_cast<const bf16x8 *>(wrow + 32 * ks);
+            const bf16x8 wm = *reinterpret_cast<const bf16x8 *>(wrow + WPLANE + 32 * ks);
+            const bf16x8 wo = *reinterpret_cast<const bf16x8 *>(wrow + 2 * WPLANE + 32 * ks);
+            main = mfma_bf16(wh, ub[0][ks], main);
+            small = mfma_bf16(wm, ub[0][ks], small);
+            small = mfma_bf16(wh, ub[1][ks], small);
+            small = mfma_bf16(wo, ub[0][ks], small);
+            small = mfma_bf16(wh, ub[2][ks], small);
+            small = mfma_bf16(wm, ub[1][ks], small);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) xv[mt][i] = xv[mt][i] - (main[i] + small[i]);
+    }
+    if (a.rotated && orow >= 0) {
+#pragma unroll
+        for (int mt = 0; mt < MTG; mt++)
+            *reinterpret_cast<float4 *>(a.rotated + tok * a.n + c0 + 16 * mt + 4 * g) =
+                make_float4(xv[mt][0], xv[mt][1], xv[mt][2], xv[mt][3]);
+    }
+    // the group of token c16 is spread over lanes c16 + 16g
+    float lo = xv[0][0], hi = lo;
+#pragma unroll
+    for (int mt = 0; mt < MTG; mt++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) { lo = fminf(lo, xv[mt][i]); hi = fmaxf(hi, xv[mt][i]); }
+    lo = fminf(lo, __shfl_xor(lo, 16)); hi = fmaxf(hi, __shfl_xor(hi, 16));
+    lo = fminf(lo, __shfl_xor(lo, 32)); hi = fmaxf(hi, __shfl_xor(hi, 32));
+    const GroupParams gp = group_params(lo, hi);
+    const float rs = 1.0f / gp.s;
+    bool tie = false;
+    uint32_t q16[MTG];
+#pragma unroll
+    for (int mt = 0; mt < MTG; mt++) {
+        q16[mt] = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) q16[mt] |= quant_code_fast(xv[mt][i], gp.z, rs, tie) << (4 * i);
+    }
+    if (__builtin_expect(__any(tie), 0)) {
+#pragma unroll
+        for (int mt = 0; mt < MTG; mt++) {
+            q16[mt] = 0;
+#pragma unroll
+            for (int i = 0; i < 4; i++) q16[mt] |= quant_code(xv[mt][i], gp) << (4 * i);
+        }
+    }
+#pragma unroll
+    for (int mt = 0; mt < MTG; mt++) cst[c16][4 * mt + g] = (uint16_t)q16[mt];
+    if (g == 0 && orow >= 0) {
+        const int64_t gi = orow * (a.n / B) + c0 / B;
+        a.scales[gi] = gp.s16;
+        a.zeros[gi] = gp.z16;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // store: four lanes per token, B/8 bytes each
+    if (srow >= 0) {
+        const int tl = lane >> 2, qt = lane & 3;
+        uint8_t *dst = a.codes + srow * (a.n / 2) + c0 / 2 + qt * (B / 8);
+        const uint16_t *src = &cst[tl][qt * (B / 16)];
+        if constexpr (B == 128) {
+            const uint2 *s2 = reinterpret_cast<const uint2 *>(src);
+            reinterpret_cast<uint4 *>(dst)[0] = make_uint4(s2[0].x, s2[0].y, s2[1].x, s2[1].y);
+        } else if constexpr (B == 64) {
+            reinterpret_cast<uint2 *>(dst)[0] = *reinterpret_cast<const uint2 *>(src);
+        } else {
+            reinterpret_cast<uint32_t *>(dst)[0] = *reinterpret_cast<const uint32_t *>(src);
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// grid (8 * ncb * ceil(token groups / 8)), block 256.  A workgroup owns CW
+// channels: it stages their W^T terms in LDS once ([3][CW][KP], 48 KB) and
+// then runs a.tpw tiles of 128 tokens over them.  Within a tile every wave
+// works alone (no further workgroup barriers) on 32 tokens x CW channels as a
+// sequence of units (group, 16-token half); the P loads of the next unit are
+// issued before the current one is processed (two register buffers used
+// alternately, scheduling fences keeping each unit's loads together).
+// Workgroups are dispatched to the 8 XCDs round-robin by block id, so the
+// token group is chosen from (id % 8) and the channel block from the quotient:
+// all channel blocks of a token group run on one XCD, and the 2-byte scale and
+// zero stores of those tokens merge into whole lines in that XCD's L2.
+template <int B, int KS, int CW>
+__global__ void __launch_bounds__(256, 2)
 corr_quant_kernel(CorrQuantArgs a)
 {
     constexpr int KP = 32 * KS;
-    constexpr int MTG = B / 16;            // M tiles per group
-    constexpr int NT = 2;                  // 16-token N tiles per wave
-    constexpr int RW = B / 4 + 4;          // uint16 slots per token row of the code stage (8-byte rows)
-    __shared__ __align__(16) uint16_t cst[4][16 * NT][RW];
+    constexpr int WPLANE = CW * KP;
+    constexpr int UNITS = 2 * (CW / B);
+    __shared__ __align__(16) __bf16 ws[3 * WPLANE];
+    __shared__ __align__(16) uint16_t cst[4][16][B / 4 + 4];
     const int tid = threadIdx.x;
     const int lane = tid & 63, w = tid >> 6;
     const int g = lane >> 4, c16 = lane & 15;
-    const int64_t cb = (int64_t)blockIdx.x % a.ncb;
-    const int64_t tb = (int64_t)blockIdx.x / a.ncb;
-    const int64_t t0 = tb * 128 + w * 32;
-    if (t0 >= a.T) return;
+    const int64_t j = (int64_t)blockIdx.x / 8;
+    const int64_t cb = j % a.ncb;
+    const int64_t tg = (j / a.ncb) * 8 + blockIdx.x % 8;
+    if (tg * a.tpw * 128 >= a.T) return;
+    const int64_t cbeg = cb * CW;
     const int64_t plane = (int64_t)KP * a.n;
-    const int64_t gpt = a.n / B;
 
-    int64_t tok[NT], orow[NT];
-    bf16x8 ub[3][NT][KS];
-#pragma unroll
-    for (int nt = 0; nt < NT; nt++) {
-        const int64_t t = t0 + 16 * nt + c16;
-        tok[nt] = t < a.T ? t : a.T - 1;
-        orow[nt] = t < a.T ? (a.dest ? a.dest[t] : t) : -1;
-#pragma unroll
-        for (int term = 0; term < 3; term++)
-#pragma unroll
-            for (int ks = 0; ks < KS; ks++)
-                ub[term][nt][ks] = load_bf16x8(a.u3 + (tok[nt] * 3 + term) * KP + 32 * ks + 8 * g);
+    for (int p = tid; p < 3 * WPLANE / 8; p += 256) {
+        const int term = p / (WPLANE / 8), rem = p % (WPLANE / 8);
+        *reinterpret_cast<bf16x8 *>(&ws[term * WPLANE + rem * 8]) =
+            load_bf16x8(a.wtt + term * plane + cbeg * KP + rem * 8);
     }
+    __syncthreads();
 
-    for (int64_t c0 = cb * a.cw; c0 < (cb + 1) * a.cw; c0 += B) {
-        float xv[MTG][NT][4];
+    for (int tt = 0; tt < a.tpw; tt++) {
+        const int64_t t0 = (tg * a.tpw + tt) * 128 + w * 32;
+        if (t0 >= a.T) return;
+        int64_t tok[2], orow[2], srow[2];
+        bf16x8 ub[2][3][KS];
+        const float *prow[2];
 #pragma unroll
-        for (int mt = 0; mt < MTG; mt++)
+        for (int nt = 0; nt < 2; nt++) {
+            const int64_t t = t0 + 16 * nt + c16;
+            tok[nt] = t < a.T ? t : a.T - 1;
+            orow[nt] = t < a.T ? (a.dest ? a.dest[t] : t) : -1;
+            const int64_t ts = t0 + 16 * nt + (lane >> 2);
+            srow[nt] = ts < a.T ? (a.dest ? a.dest[ts] : ts) : -1;
+            prow[nt] = a.P + tok[nt] * a.n + cbeg + 4 * g;
 #pragma unroll
-            for (int nt = 0; nt < NT; nt++) {
-                const float4 pv = *reinterpret_cast<const float4 *>(a.P + tok[nt] * a.n + c0 + 16 * mt + 4 * g);
-                xv[mt][nt][0] = pv.x; xv[mt][nt][1] = pv.y; xv[mt][nt][2] = pv.z; xv[mt][nt][3] = pv.w;
-            }
+            for (int term = 0; term < 3; term++)
 #pragma unroll
-        for (int mt = 0; mt < MTG; mt++) {
-            const __bf16 *wrow = a.wtt + (c0 + 16 * mt + c16) * KP + 8 * g;
-            bf16x8 wh[KS], wm[KS], wl[KS];
-#pragma unroll
-            for (int ks = 0; ks < KS; ks++) {
-                wh[ks] = load_bf16x8(wrow + 32 * ks);
-                wm[ks] = load_bf16x8(wrow + plane + 32 * ks);
-                wl[ks] = load_bf16x8(wrow + 2 * plane + 32 * ks);
-            }
-#pragma unroll
-            for (int nt = 0; nt < NT; nt++) {
-                floatx4 main = zero4(), small = zero4();
-#pragma unroll
-                for (int ks = 0; ks < KS; ks++) {
-                    main = mfma_bf16(wh[ks], ub[0][nt][ks], main);
-                    small = mfma_bf16(wm[ks], ub[0][nt][ks], small);
-                    small = mfma_bf16(wh[ks], ub[1][nt][ks], small);
-                    small = mfma_bf16(wl[ks], ub[0][nt][ks], small);
-                    small = mfma_bf16(wh[ks], ub[2][nt][ks], small);
-                    small = mfma_bf16(wm[ks], ub[1][nt][ks], small);
-                }
-#pragma unroll
-                for (int i = 0; i < 4; i++) xv[mt][nt][i] = xv[mt][nt][i] - (main[i] + small[i]);
-            }
+                for (int ks = 0; ks < KS; ks++)
+                    ub[nt][term][ks] = load_bf16x8(a.u3 + (tok[nt] * 3 + term) * KP + 32 * ks + 8 * g);
         }
-        if (a.rotated) {
-#pragma unroll
-            for (int nt = 0; nt < NT; nt++)
-                if (orow[nt] >= 0)
-#pragma unroll
-                    for (int mt = 0; mt < MTG; mt++)
-                        *reinterpret_cast<float4 *>(a.rotated + tok[nt] * a.n + c0 + 16 * mt + 4 * g) =
-                            make_float4(xv[mt][nt][0], xv[mt][nt][1], xv[mt][nt][2], xv[mt][nt][3]);
+        // unit u: group u / 2, token half u % 2
+        CqUnit<B> xa, xb;
+        cq_load<B>(xa, prow[0]);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll 1
+        for (int u = 0; u < UNITS; u += 2) {
+            const int cg = (u / 2) * B;
+            cq_load<B>(xb, prow[1] + cg);
+            __builtin_amdgcn_sched_barrier(0);
+            cq_unit<B, KS, WPLANE>(xa, a, ub[0], tok[0], orow[0], srow[0], cbeg + cg, ws + cg * KP, cst[w], lane);
+            __builtin_amdgcn_sched_barrier(0);
+            if (u + 2 < UNITS) cq_load<B>(xa, prow[0] + cg + B);
+            __builtin_amdgcn_sched_barrier(0);
+            cq_unit<B, KS, WPLANE>(xb, a, ub[1], tok[1], orow[1], srow[1], cbeg + cg, ws + cg * KP, cst[w], lane);
+            __builtin_amdgcn_sched_barrier(0);
         }
-        // quantize: the group of token (nt, c16) is spread over lanes c16 + 16g
-#pragma unroll
-        for (int nt = 0; nt < NT; nt++) {
-            float lo = xv[0][nt][0], hi = lo;
-#pragma unroll
-            for (int mt = 0; mt < MTG; mt++)
-#pragma unroll
-                for (int i = 0; i < 4; i++) { lo = fminf(lo, xv[mt][nt][i]); hi = fmaxf(hi, xv[mt][nt][i]); }
-            lo = fminf(lo, __shfl_xor(lo, 16)); hi = fmaxf(hi, __shfl_xor(hi, 16));
-            lo = fminf(lo, __shfl_xor(lo, 32)); hi = fmaxf(hi, __shfl_xor(hi, 32));
-            const GroupParams gp = group_params(lo, hi);
-            const float rs = 1.0f / gp.s;
-            bool tie = false;
-            uint32_t q16[MTG];
-#pragma unroll
-            for (int mt = 0; mt < MTG; mt++) {
-                q16[mt] = 0;
-#pragma unroll
-                for (int i = 0; i < 4; i++) q16[mt] |= quant_code_fast(xv[mt][nt][i], gp.z, rs, tie) << (4 * i);
-            }
-            if (__builtin_expect(__any(tie), 0)) {
-#pragma unroll
-                for (int mt = 0; mt < MTG; mt++) {
-                    q16[mt] = 0;
-#pragma unroll
-                    for (int i = 0; i < 4; i++) q16[mt] |= quant_code(xv[mt][nt][i], gp) << (4 * i);
-                }
-            }
-#pragma unroll
-            for (int mt = 0; mt < MTG; mt++) cst[w][16 * nt + c16][4 * mt + g] = (uint16_t)q16[mt];
-            if (g == 0 && orow[nt] >= 0) {
-                const int64_t gi = orow[nt] * gpt + c0 / B;
-                a.scales[gi] = gp.s16;
-                a.zeros[gi] = gp.z16;
-            }
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        // store: two lanes per token, B/4 bytes each
-        {
-            const int tl = lane >> 1, half = lane & 1;
-            const int64_t t = t0 + tl;
-            const uint16_t *src = &cst[w][tl][half * (B / 8)];
-            if (t < a.T) {
-                const int64_t r = a.dest ? a.dest[t] : t;
-                uint8_t *dst = a.codes + r * (a.n / 2) + c0 / 2 + half * (B / 4);
-                if constexpr (B == 128) {
-                    const uint2 *s2 = reinterpret_cast<const uint2 *>(src);
-                    uint4 v0 = make_uint4(s2[0].x, s2[0].y, s2[1].x, s2[1].y);
-                    uint4 v1 = make_uint4(s2[2].x, s2[2].y, s2[3].x, s2[3].y);
-                    reinterpret_cast<uint4 *>(dst)[0] = v0;
-                    reinterpret_cast<uint4 *>(dst)[1] = v1;
-                } else if constexpr (B == 64) {
-                    const uint2 *s2 = reinterpret_cast<const uint2 *>(src);
-                    reinterpret_cast<uint4 *>(dst)[0] = make_uint4(s2[0].x, s2[0].y, s2[1].x, s2[1].y);
-                } else {
-                    const uint2 *s2 = reinterpret_cast<const uint2 *>(src);
-                    reinterpret_cast<uint2 *>(dst)[0] = s2[0];
-                }
-            }
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
 }
 

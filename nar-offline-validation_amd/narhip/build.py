@@ -8,6 +8,9 @@ hipcc flags:
   -fhip-fp32-correctly-rounded-divide-sqrt, -fno-gpu-flush-denormals-to-zero
                                  IEEE fp32 division and denormals, as the
                                  reference's fp32 arithmetic on the CPU
+  -mllvm -amdgpu-mfma-vgpr-form=1
+                                 MFMA results in ordinary VGPRs (no accvgpr
+                                 moves between the matrix and vector stages)
 """
 
 from __future__ import annotations
@@ -27,7 +30,8 @@ FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-ffp-contract=off", "-fhip-fp32-correctly-rounded-divide-sqrt",
-    "-fno-gpu-flush-denormals-to-zero", "-Wall", "-Wno-unused-function",
+    "-fno-gpu-flush-denormals-to-zero", "-mllvm", "-amdgpu-mfma-vgpr-form=1",
+    "-Wall", "-Wno-unused-function",
 ]
 
 
