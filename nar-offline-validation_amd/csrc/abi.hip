@@ -180,13 +180,13 @@ int launch_row_mqb(const RowArgs &a, hipStream_t s)
 template <int M, int Q, int B>
 int launch_kron_mqb(const KronArgs &a, bool quant, hipStream_t s)
 {
-    const size_t lds = sizeof(float) * M * Q;
+    const size_t lds = sizeof(float) * M * (Q + KPAD);
     if (quant) {
         if (int rc = set_lds(&kron_mfma_kernel<M, Q, B, true>, lds)) return rc;
-        hipLaunchKernelGGL((kron_mfma_kernel<M, Q, B, true>), dim3((unsigned)a.T), dim3(256), lds, s, a);
+        hipLaunchKernelGGL((kron_mfma_kernel<M, Q, B, true>), dim3((unsigned)a.T), dim3(16 * M), lds, s, a);
     } else {
         if (int rc = set_lds(&kron_mfma_kernel<M, Q, 128, false>, lds)) return rc;
-        hipLaunchKernelGGL((kron_mfma_kernel<M, Q, 128, false>), dim3((unsigned)a.T), dim3(256), lds, s, a);
+        hipLaunchKernelGGL((kron_mfma_kernel<M, Q, 128, false>), dim3((unsigned)a.T), dim3(16 * M), lds, s, a);
     }
     return check_launch("kron_mfma_kernel");
 }
@@ -265,13 +265,13 @@ int launch_prepare(const float *v, const float *wt, int64_t n, int k, void *prep
     return NARHIP_OK;
 }
 
-// Channel splits for the MFMA projection: enough workgroups to cover the GPU
+// Channel splits for the MFMA projection: enough workgroups for two per CU
 // (256-token tiles, splits of a multiple of 128 channels).
 int mfma_splits(int64_t T, int64_t n)
 {
     const int64_t tiles = (T + 255) / 256;
     int s = 1;
-    while (s < 64 && tiles * s < 512 && n % (256 * (int64_t)s) == 0) s *= 2;
+    while (s < 64 && tiles * s < 1024 && n % (128 * 2 * (int64_t)s) == 0) s *= 2;
     return s;
 }
 
@@ -303,18 +303,18 @@ int launch_fold_u(const float *partial, int splits, int k, int kp, int64_t T, __
     return check_launch("fold_u_kernel");
 }
 
+// u terms [T][3][kp32] bf16, then a scratch row of n/2 bytes for the stores of
+// out-of-range tokens of the last tile (n/2 + 4 KB: codes, scales, rotated x')
 size_t u3_bytes(int64_t T, int k) { return sizeof(uint16_t) * 3 * (size_t)kp32(k) * (size_t)T; }
+size_t corr_scratch_bytes(int64_t T, int64_t n, int k) { return align256(u3_bytes(T, k)) + align256((size_t)n / 2 + 4096); }
 
 template <int B, int KS, int CW>
 int launch_cq(const CorrQuantArgs &a, dim3 grid, hipStream_t s)
 {
-    hipLaunchKernelGGL((corr_quant_kernel<B, KS, CW>), grid, dim3(256), 0, s, a);
+    if (a.rotated) hipLaunchKernelGGL((corr_quant_kernel<B, KS, CW, true>), grid, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((corr_quant_kernel<B, KS, CW, false>), grid, dim3(256), 0, s, a);
     return check_launch("corr_quant_kernel");
 }
-
-#ifndef NARHIP_CQ_CW_K32
-#define NARHIP_CQ_CW_K32 256
-#endif
 
 template <int B>
 int launch_cq_b(const CorrQuantArgs &a, int ks, int cw, dim3 grid, hipStream_t s)
@@ -330,7 +330,7 @@ int launch_corr_quant(CorrQuantArgs a, int b, hipStream_t s)
 {
     if (a.T == 0) return NARHIP_OK;
     const int ks = a.kp / 32;
-    const int cw = (ks == 1 && a.n % 256 == 0) ? NARHIP_CQ_CW_K32 : 128;
+    const int cw = (ks == 1 && a.n % 256 == 0) ? 256 : 128;
     if (a.n % cw || cw % b) return fail(NARHIP_EUNSUPPORTED, "rank correction needs n %% 128 == 0");
     a.ncb = a.n / cw;
     const int64_t tiles = (a.T + 127) / 128;
@@ -428,7 +428,7 @@ int make_plan(int64_t T, int64_t n, int m, int q, int k, int64_t nb, bool have_p
         p.proj_b = p.need_proj ? sizeof(float) * (size_t)p.chunk * (size_t)p.splits * (size_t)k : 0;
         p.need_P = true;
         p.P_b = sizeof(float) * (size_t)p.chunk * (size_t)n;
-        p.u_b = u3_bytes(p.chunk, k);
+        p.u_b = corr_scratch_bytes(p.chunk, n, k);
         return NARHIP_OK;
     }
     p.need_proj = !have_partial;
@@ -506,6 +506,7 @@ int run_rotate_quant(const void *x_bf16, int64_t T, int64_t n, int64_t ldx, int 
             if ((rc = launch_fold_u(part, sp, k, kp32(k), tn, u3, s))) return rc;
             CorrQuantArgs ca{};
             ca.P = Pbuf; ca.T = tn; ca.n = n; ca.u3 = u3;
+            ca.dummy = reinterpret_cast<uint8_t *>(u3) + align256(u3_bytes(tn, k));
             ca.wtt = reinterpret_cast<const __bf16 *>(static_cast<const char *>(prep) + vt_bytes(n, k));
             ca.kp = kp32(k);
             ca.dest = dest ? dest + t0 : nullptr;

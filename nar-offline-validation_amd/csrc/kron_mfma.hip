@@ -1,6 +1,6 @@
 // Kronecker row transform with the Paley factor on bf16 MFMA.
 //
-// One workgroup per token (4 waves, 16 rows of 16 lanes):
+// One workgroup per token, one 16-lane row per segment (16 M threads):
 //   phase 1  F[a, :] = FWHT_Q(x[a*Q:(a+1)*Q]) / fp32(sqrt(Q))   (DPP, as rq_row.hip)
 //   phase 2  P[a, c] = hm * S[a, c],  S = Hm(+-1) F                  (MFMA)
 //            F enters as three exact bf16 terms; S1 = Hm F_hi and S23 = Hm (F_mid + F_lo)
@@ -28,14 +28,21 @@ struct KronArgs {
     float sq, rsq, hm;     // fp32(sqrt(Q)), RN(1/sq), RN(1/fp32(sqrt(M)))
 };
 
+// Rows of F in LDS are padded by KPAD floats, so that the column accesses of
+// phase 2 (lanes of a wave read rows 8 apart) fall in different banks.
+constexpr int KPAD = 4;
+
 template <int M, int Q, int B, bool QUANT>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(16 * M)
 kron_mfma_kernel(KronArgs a)
 {
     constexpr int NH = Q / 128;
     constexpr int NV = 8 * NH;
     constexpr int N = M * Q;
+    constexpr int QS = Q + KPAD;            // LDS row stride (floats)
     constexpr int NMT = (M + 15) / 16;
+    constexpr int NT = 16 * M;              // threads: one 16-lane row per segment
+    constexpr int NW = NT / 64;             // waves
     extern __shared__ float F[];
     const int tid = threadIdx.x;
     const int l16 = tid & 15;
@@ -44,16 +51,27 @@ kron_mfma_kernel(KronArgs a)
     const int64_t t = blockIdx.x;
     const uint16_t *xt = a.x + t * a.ldx;
 
-    // ---- phase 1 (identical arithmetic to rq_row_kernel)
-    for (int s = row; s < M; s += 16) {
+    // Paley rows as the MFMA A operand (issued first; used after phase 1)
+    const int lane = tid & 63, wv = tid >> 6;
+    const int g = lane >> 4, c16 = lane & 15;
+    uint32_t negbits[NMT];
+#pragma unroll
+    for (int mt = 0; mt < NMT; mt++) {
+        const int r = 16 * mt + c16;
+        negbits[mt] = r < M ? a.paley.neg[r] : 0u;
+    }
+
+    // ---- phase 1 (identical arithmetic to rq_row_kernel): row `row` transforms segment `row`
+    {
+        const int s = row;
         float v[NV];
 #pragma unroll
         for (int h = 0; h < NH; h++) {
-            uint4 wv = *reinterpret_cast<const uint4 *>(xt + s * Q + h * 128 + chunk * 8);
-            v[h * 8 + 0] = bf16lo(wv.x); v[h * 8 + 1] = bf16hi(wv.x);
-            v[h * 8 + 2] = bf16lo(wv.y); v[h * 8 + 3] = bf16hi(wv.y);
-            v[h * 8 + 4] = bf16lo(wv.z); v[h * 8 + 5] = bf16hi(wv.z);
-            v[h * 8 + 6] = bf16lo(wv.w); v[h * 8 + 7] = bf16hi(wv.w);
+            uint4 xw = *reinterpret_cast<const uint4 *>(xt + s * Q + h * 128 + chunk * 8);
+            v[h * 8 + 0] = bf16lo(xw.x); v[h * 8 + 1] = bf16hi(xw.x);
+            v[h * 8 + 2] = bf16lo(xw.y); v[h * 8 + 3] = bf16hi(xw.y);
+            v[h * 8 + 4] = bf16lo(xw.z); v[h * 8 + 5] = bf16hi(xw.z);
+            v[h * 8 + 6] = bf16lo(xw.w); v[h * 8 + 7] = bf16hi(xw.w);
         }
         if (a.signs) {
 #pragma unroll
@@ -100,7 +118,7 @@ kron_mfma_kernel(KronArgs a)
         div_sqrt_q<Q>(v, a.sq, a.rsq);
 #pragma unroll
         for (int h = 0; h < NH; h++) {
-            float4 *d = reinterpret_cast<float4 *>(F + s * Q + h * 128 + chunk * 8);
+            float4 *d = reinterpret_cast<float4 *>(F + s * QS + h * 128 + chunk * 8);
             d[0] = make_float4(v[h * 8 + 0], v[h * 8 + 1], v[h * 8 + 2], v[h * 8 + 3]);
             d[1] = make_float4(v[h * 8 + 4], v[h * 8 + 5], v[h * 8 + 6], v[h * 8 + 7]);
         }
@@ -109,29 +127,26 @@ kron_mfma_kernel(KronArgs a)
 
     // ---- phase 2: Paley product on MFMA, one 16-column block at a time, in place
     {
-        const int lane = tid & 63, wv = tid >> 6;
-        const int g = lane >> 4, c16 = lane & 15;
         bf16x8 ha[NMT];
 #pragma unroll
         for (int mt = 0; mt < NMT; mt++) {
-            const int r = 16 * mt + c16;
 #pragma unroll
             for (int j = 0; j < 8; j++) {
                 const int c = 8 * g + j;
                 float e = 0.0f;
-                if (r < M && c < M) e = ((a.paley.neg[r] >> c) & 1u) ? -1.0f : 1.0f;
+                if (16 * mt + c16 < M && c < M) e = ((negbits[mt] >> c) & 1u) ? -1.0f : 1.0f;
                 ha[mt][j] = (__bf16)e;
             }
         }
         const float hm = a.hm;
         constexpr int CB = Q / 16;
-        for (int cb = wv; cb < CB; cb += 4) {
+        for (int cb = wv; cb < CB; cb += NW) {
             const int c = 16 * cb + c16;
             float f[8];
 #pragma unroll
             for (int j = 0; j < 8; j++) {
                 const int ar = 8 * g + j;
-                f[j] = ar < M ? F[ar * Q + c] : 0.0f;
+                f[j] = ar < M ? F[ar * QS + c] : 0.0f;
             }
             bf16x8 bh, bm, bl;
             split3x8(f, bh, bm, bl);
@@ -143,32 +158,34 @@ kron_mfma_kernel(KronArgs a)
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     const int ar = 16 * mt + 4 * g + i;
-                    if (ar < M) F[ar * Q + c] = __builtin_fmaf(hm, s1[i], hm * s2[i]);
+                    if (ar < M) F[ar * QS + c] = __builtin_fmaf(hm, s1[i], hm * s2[i]);
                 }
             }
         }
     }
     __syncthreads();
 
+    // row-major float4 index i of the token's N floats -> its place in F
+    auto fidx = [](int i) { return (i / (Q / 4)) * QS + (i % (Q / 4)) * 4; };
     if constexpr (!QUANT) {
         float4 *dst = reinterpret_cast<float4 *>(a.P + t * N);
-        for (int i = tid; i < N / 4; i += 256) dst[i] = reinterpret_cast<const float4 *>(F)[i];
+        for (int i = tid; i < N / 4; i += NT) dst[i] = *reinterpret_cast<const float4 *>(F + fidx(i));
         return;
     } else {
         if (a.rotated) {
-            for (int i = tid; i < N / 4; i += 256)
-                reinterpret_cast<float4 *>(a.rotated + t * N)[i] = reinterpret_cast<const float4 *>(F)[i];
+            for (int i = tid; i < N / 4; i += NT)
+                reinterpret_cast<float4 *>(a.rotated + t * N)[i] = *reinterpret_cast<const float4 *>(F + fidx(i));
         }
         constexpr int G8 = B / 8;
         constexpr int CHUNKS = N / 8;
         const int64_t orow = a.dest ? a.dest[t] : t;
-        for (int c0 = 0; c0 < CHUNKS; c0 += 256) {
+        for (int c0 = 0; c0 < CHUNKS; c0 += NT) {
             const int ch = c0 + tid;
             const bool ok = ch < CHUNKS;
             const int chs = ok ? ch : 0;
             float v[8];
             {
-                const float4 *s = reinterpret_cast<const float4 *>(F + chs * 8);
+                const float4 *s = reinterpret_cast<const float4 *>(F + fidx(2 * chs));
                 float4 p0 = s[0], p1 = s[1];
                 v[0] = p0.x; v[1] = p0.y; v[2] = p0.z; v[3] = p0.w;
                 v[4] = p1.x; v[5] = p1.y; v[6] = p1.z; v[7] = p1.w;

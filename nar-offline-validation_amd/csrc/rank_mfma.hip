@@ -164,7 +164,8 @@ struct CorrQuantArgs {
     uint16_t *scales;
     uint16_t *zeros;
     const int64_t *dest;
-    float *rotated;        // optional x' [T, n]
+    float *rotated;        // x' [T, n] (kernel variant ROT only)
+    uint8_t *dummy;        // scratch row (>= n/2 bytes) that takes the stores of tokens >= T
     int64_t ncb;           // n / CW channel blocks
     int tpw;               // 128-token tiles per workgroup
 };
@@ -188,12 +189,12 @@ __device__ __forceinline__ void cq_load(CqUnit<B> &p, const float *prow)
 }
 
 // x' = P - u W^T for one unit (W^T terms of the group at wl in LDS, planes of
-// WPLANE elements), then its codes (staged through the wave's LDS rows cst),
-// scales and zeros.  srow: output row of token lane/4 for the code store.
-template <int B, int KS, int WPLANE>
+// WPLANE elements), then its codes, scales and zeros, staged in LDS: codes of
+// token c16 at crow[c16 * CSTRIDE + ...] (uint16 = four codes), scale and zero
+// at sz[2 c16], sz[2 c16 + 1].  Only x' (variant ROT) goes to memory here.
+template <int B, int KS, int WPLANE, int CSTRIDE, bool ROT>
 __device__ __forceinline__ void cq_unit(CqUnit<B> &xt, const CorrQuantArgs &a, const bf16x8 (&ub)[3][KS],
-                                        int64_t tok, int64_t orow, int64_t srow, int64_t c0,
-                                        const __bf16 *wl, uint16_t (*cst)[B / 4 + 4], int lane)
+                                        float *rrow, const __bf16 *wl, uint16_t *crow, uint16_t *sz, int lane)
 {
     constexpr int KP = 32 * KS;
     constexpr int MTG = B / 16;
@@ -218,11 +219,10 @@ __device__ __forceinline__ void cq_unit(CqUnit<B> &xt, const CorrQuantArgs &a, c
 #pragma unroll
         for (int i = 0; i < 4; i++) xv[mt][i] = xv[mt][i] - (main[i] + small[i]);
     }
-    if (a.rotated && orow >= 0) {
+    if constexpr (ROT) {
 #pragma unroll
         for (int mt = 0; mt < MTG; mt++)
-            *reinterpret_cast<float4 *>(a.rotated + tok * a.n + c0 + 16 * mt + 4 * g) =
-                make_float4(xv[mt][0], xv[mt][1], xv[mt][2], xv[mt][3]);
+            *reinterpret_cast<float4 *>(rrow + 16 * mt) = make_float4(xv[mt][0], xv[mt][1], xv[mt][2], xv[mt][3]);
     }
     // the group of token c16 is spread over lanes c16 + 16g
     float lo = xv[0][0], hi = lo;
@@ -251,54 +251,37 @@ __device__ __forceinline__ void cq_unit(CqUnit<B> &xt, const CorrQuantArgs &a, c
         }
     }
 #pragma unroll
-    for (int mt = 0; mt < MTG; mt++) cst[c16][4 * mt + g] = (uint16_t)q16[mt];
-    if (g == 0 && orow >= 0) {
-        const int64_t gi = orow * (a.n / B) + c0 / B;
-        a.scales[gi] = gp.s16;
-        a.zeros[gi] = gp.z16;
+    for (int mt = 0; mt < MTG; mt++) crow[c16 * CSTRIDE + 4 * mt + g] = (uint16_t)q16[mt];
+    if (g == 0) {
+        sz[2 * c16] = gp.s16;
+        sz[2 * c16 + 1] = gp.z16;
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    // store: four lanes per token, B/8 bytes each
-    if (srow >= 0) {
-        const int tl = lane >> 2, qt = lane & 3;
-        uint8_t *dst = a.codes + srow * (a.n / 2) + c0 / 2 + qt * (B / 8);
-        const uint16_t *src = &cst[tl][qt * (B / 16)];
-        if constexpr (B == 128) {
-            const uint2 *s2 = reinterpret_cast<const uint2 *>(src);
-            reinterpret_cast<uint4 *>(dst)[0] = make_uint4(s2[0].x, s2[0].y, s2[1].x, s2[1].y);
-        } else if constexpr (B == 64) {
-            reinterpret_cast<uint2 *>(dst)[0] = *reinterpret_cast<const uint2 *>(src);
-        } else {
-            reinterpret_cast<uint32_t *>(dst)[0] = *reinterpret_cast<const uint32_t *>(src);
-        }
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
 // grid (8 * ncb * ceil(token groups / 8)), block 256.  A workgroup owns CW
 // channels: it stages their W^T terms in LDS once ([3][CW][KP], 48 KB) and
 // then runs a.tpw tiles of 128 tokens over them.  Within a tile every wave
-// works alone (no further workgroup barriers) on 32 tokens x CW channels as a
-// sequence of units (group, 16-token half); the P loads of the next unit are
-// issued before the current one is processed (two register buffers used
-// alternately, scheduling fences keeping each unit's loads together).
+// works alone (no further workgroup barriers) on 32 tokens x CW channels:
+// all of its P (128 VGPRs at CW = 256) is requested at once, then the units
+// (group gi, 16-token half h) are processed in load order, each waiting only
+// for its own loads.  Codes, scales and zeros are staged in LDS and stored
+// after the last unit; tokens >= T store into a scratch row, so that no
+// memory operation sits under a branch and the wait counts stay exact.
 // Workgroups are dispatched to the 8 XCDs round-robin by block id, so the
 // token group is chosen from (id % 8) and the channel block from the quotient:
 // all channel blocks of a token group run on one XCD, and the 2-byte scale and
 // zero stores of those tokens merge into whole lines in that XCD's L2.
-template <int B, int KS, int CW>
+template <int B, int KS, int CW, bool ROT>
 __global__ void __launch_bounds__(256, 2)
 corr_quant_kernel(CorrQuantArgs a)
 {
     constexpr int KP = 32 * KS;
     constexpr int WPLANE = CW * KP;
-    constexpr int UNITS = 2 * (CW / B);
+    constexpr int NG = CW / B;               // groups per channel block
+    constexpr int CSTRIDE = CW / 4 + 8;      // uint16 per token row of staged codes (16-byte rows)
     __shared__ __align__(16) __bf16 ws[3 * WPLANE];
-    __shared__ __align__(16) uint16_t cst[4][16][B / 4 + 4];
+    __shared__ __align__(16) uint16_t cst[4][32 * CSTRIDE];
+    __shared__ __align__(16) uint16_t szs[4][NG][64];   // [2 t + 0] scale, [2 t + 1] zero of token t
     const int tid = threadIdx.x;
     const int lane = tid & 63, w = tid >> 6;
     const int g = lane >> 4, c16 = lane & 15;
@@ -319,39 +302,72 @@ corr_quant_kernel(CorrQuantArgs a)
     for (int tt = 0; tt < a.tpw; tt++) {
         const int64_t t0 = (tg * a.tpw + tt) * 128 + w * 32;
         if (t0 >= a.T) return;
-        int64_t tok[2], orow[2], srow[2];
-        bf16x8 ub[2][3][KS];
+        // output rows: code stores (token lane/2), scale stores (token lane, lanes < 32)
+        const int64_t tc = t0 + (lane >> 1), ts = t0 + (lane & 31);
+        int64_t crow_out = tc < a.T ? tc : -1, srow_out = ts < a.T ? ts : -1;
+        if (a.dest) {
+            if (crow_out >= 0) crow_out = a.dest[crow_out];
+            if (srow_out >= 0) srow_out = a.dest[srow_out];
+        }
         const float *prow[2];
+        float *rrow[2];
+        bf16x8 ub[2][3][KS];
 #pragma unroll
-        for (int nt = 0; nt < 2; nt++) {
-            const int64_t t = t0 + 16 * nt + c16;
-            tok[nt] = t < a.T ? t : a.T - 1;
-            orow[nt] = t < a.T ? (a.dest ? a.dest[t] : t) : -1;
-            const int64_t ts = t0 + 16 * nt + (lane >> 2);
-            srow[nt] = ts < a.T ? (a.dest ? a.dest[ts] : ts) : -1;
-            prow[nt] = a.P + tok[nt] * a.n + cbeg + 4 * g;
+        for (int h = 0; h < 2; h++) {
+            const int64_t t = t0 + 16 * h + c16;
+            const int64_t tk = t < a.T ? t : a.T - 1;
+            prow[h] = a.P + tk * a.n + cbeg + 4 * g;
+            rrow[h] = ROT ? (t < a.T ? a.rotated + tk * a.n + cbeg + 4 * g
+                                     : reinterpret_cast<float *>(a.dummy) + 4 * g) : nullptr;
 #pragma unroll
             for (int term = 0; term < 3; term++)
 #pragma unroll
                 for (int ks = 0; ks < KS; ks++)
-                    ub[nt][term][ks] = load_bf16x8(a.u3 + (tok[nt] * 3 + term) * KP + 32 * ks + 8 * g);
+                    ub[h][term][ks] = load_bf16x8(a.u3 + (tk * 3 + term) * KP + 32 * ks + 8 * g);
         }
-        // unit u: group u / 2, token half u % 2
-        CqUnit<B> xa, xb;
-        cq_load<B>(xa, prow[0]);
+        CqUnit<B> U[NG][2];
+#pragma unroll
+        for (int gi = 0; gi < NG; gi++)
+#pragma unroll
+            for (int h = 0; h < 2; h++) cq_load<B>(U[gi][h], prow[h] + gi * B);
         __builtin_amdgcn_sched_barrier(0);
-#pragma unroll 1
-        for (int u = 0; u < UNITS; u += 2) {
-            const int cg = (u / 2) * B;
-            cq_load<B>(xb, prow[1] + cg);
-            __builtin_amdgcn_sched_barrier(0);
-            cq_unit<B, KS, WPLANE>(xa, a, ub[0], tok[0], orow[0], srow[0], cbeg + cg, ws + cg * KP, cst[w], lane);
-            __builtin_amdgcn_sched_barrier(0);
-            if (u + 2 < UNITS) cq_load<B>(xa, prow[0] + cg + B);
-            __builtin_amdgcn_sched_barrier(0);
-            cq_unit<B, KS, WPLANE>(xb, a, ub[1], tok[1], orow[1], srow[1], cbeg + cg, ws + cg * KP, cst[w], lane);
-            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int gi = 0; gi < NG; gi++)
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                cq_unit<B, KS, WPLANE, CSTRIDE, ROT>(U[gi][h], a, ub[h], ROT ? rrow[h] + gi * B : nullptr,
+                                                     ws + gi * B * KP, &cst[w][16 * h * CSTRIDE + gi * B / 4],
+                                                     &szs[w][gi][32 * h], lane);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        // codes: two lanes per token, CW/4 bytes each (16-byte pieces)
+        {
+            const int half = lane & 1;
+            uint8_t *base = crow_out >= 0 ? a.codes + crow_out * (a.n / 2) + cbeg / 2 : a.dummy;
+            uint4 *dst = reinterpret_cast<uint4 *>(base + half * (CW / 4));
+            const uint4 *src = reinterpret_cast<const uint4 *>(&cst[w][(lane >> 1) * CSTRIDE + half * (CW / 8)]);
+#pragma unroll
+            for (int q = 0; q < CW / 64; q++) dst[q] = src[q];
         }
+        // scales and zeros: lanes 0..31 write token lane's NG groups (lanes 32..63 repeat them)
+        {
+            uint16_t *sd = srow_out >= 0 ? a.scales + srow_out * (a.n / B) + cbeg / B
+                                         : reinterpret_cast<uint16_t *>(a.dummy);
+            uint16_t *zd = srow_out >= 0 ? a.zeros + srow_out * (a.n / B) + cbeg / B
+                                         : reinterpret_cast<uint16_t *>(a.dummy);
+            const int tl = lane & 31;
+#pragma unroll
+            for (int q = 0; q < NG; q++) {
+                sd[q] = szs[w][q][2 * tl];
+                zd[q] = szs[w][q][2 * tl + 1];
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
 }
 
