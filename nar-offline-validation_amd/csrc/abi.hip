@@ -266,12 +266,12 @@ int launch_prepare(const float *v, const float *wt, int64_t n, int k, void *prep
 }
 
 // Channel splits for the MFMA projection: enough workgroups for two per CU
-// (256-token tiles, splits of a multiple of 128 channels).
+// (128-token tiles, splits of a multiple of 128 channels).
 int mfma_splits(int64_t T, int64_t n)
 {
-    const int64_t tiles = (T + 255) / 256;
+    const int64_t tiles = (T + 127) / 128;
     int s = 1;
-    while (s < 64 && tiles * s < 1024 && n % (128 * 2 * (int64_t)s) == 0) s *= 2;
+    while (s < 64 && tiles * s < 512 && n % (128 * 2 * (int64_t)s) == 0) s *= 2;
     return s;
 }
 
@@ -285,7 +285,7 @@ int launch_proj_mfma(const uint16_t *x, int64_t T, int64_t n, int64_t ldx, const
         return fail(NARHIP_EUNSUPPORTED, "MFMA projection needs n %% (128*splits) == 0 (n=%lld, splits=%d)",
                     (long long)n, splits);
     ProjMfmaArgs a{x, ldx, T, n, static_cast<const __bf16 *>(prep), kp16(k), k, splits, n / splits, partial};
-    dim3 grid((unsigned)((T + 255) / 256), (unsigned)splits);
+    dim3 grid((unsigned)((T + 127) / 128), (unsigned)splits);
     switch (kp16(k) / 16) {
     case 1: hipLaunchKernelGGL((proj_mfma_kernel<1>), grid, dim3(256), 0, s, a); break;
     case 2: hipLaunchKernelGGL((proj_mfma_kernel<2>), grid, dim3(256), 0, s, a); break;

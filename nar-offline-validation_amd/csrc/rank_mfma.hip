@@ -58,70 +58,117 @@ struct ProjMfmaArgs {
     float *partial;        // [T, splits*k]
 };
 
-// grid (ceil(T/256), splits), block 256.  Wave w owns tokens 64w..64w+63 of the
-// 256-token tile as four 16-token N tiles; all MT rank tiles of 16 rows.  The V
-// terms of each 128-channel block are staged in LDS and read by all waves.
+// grid (ceil(T/128), splits), block 256.  Wave w owns tokens 32w..32w+31 of
+// the 128-token tile as two 16-token N tiles; all MT rank tiles of 16 rows.
+// The split's channels are walked in blocks of 128 (64 for k > 32): the V
+// terms of a block are staged in LDS (two buffers, one barrier per block) and
+// x of the next block is requested while the current block's MFMAs run.
 template <int MT>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(256, 2)
 proj_mfma_kernel(ProjMfmaArgs a)
 {
-    constexpr int KB = 128;                 // channels per LDS block
+    constexpr int KB = MT <= 2 ? 128 : 64;  // channels per block (LDS: two buffers)
     constexpr int ROWS = 16 * MT;
-    __shared__ __bf16 vs[3][ROWS][KB + 8];
+    constexpr int VSTR = KB + 8;            // padded LDS row (bf16)
+    constexpr int VPIECES = 3 * ROWS * (KB / 8);              // 16-byte pieces per block
+    constexpr int VPT = (VPIECES + 255) / 256;                // pieces per thread
+    __shared__ __align__(16) __bf16 vs[2][3][ROWS][VSTR];
     const int tid = threadIdx.x;
     const int lane = tid & 63, w = tid >> 6;
     const int g = lane >> 4, c16 = lane & 15;
-    const int64_t tbase = (int64_t)blockIdx.x * 256 + w * 64 + c16;
     const int s = blockIdx.y;
     const int64_t c_begin = (int64_t)s * a.cs;
     const int64_t plane = (int64_t)a.kp * a.n;
-    const uint16_t *xrow[4];
+    const int nblk = (int)(a.cs / KB);
+    const uint16_t *xrow[2];
 #pragma unroll
-    for (int nt = 0; nt < 4; nt++) {
-        int64_t t = tbase + 16 * nt;
+    for (int nt = 0; nt < 2; nt++) {
+        int64_t t = (int64_t)blockIdx.x * 128 + w * 32 + 16 * nt + c16;
         if (t >= a.T) t = a.T - 1;
         xrow[nt] = a.x + t * a.ldx + c_begin + 8 * g;
     }
-    floatx4 acc_h[MT][4], acc_l[MT][4];
+    auto v_src = [&](int p, int blk) -> const __bf16 * {
+        const int term = p / (ROWS * (KB / 8)), rem = p % (ROWS * (KB / 8));
+        const int r = rem / (KB / 8), c8 = rem % (KB / 8);
+        return a.vt + term * plane + (int64_t)r * a.n + c_begin + (int64_t)blk * KB + c8 * 8;
+    };
+    auto v_dst = [&](int p, int buf) -> __bf16 * {
+        const int term = p / (ROWS * (KB / 8)), rem = p % (ROWS * (KB / 8));
+        const int r = rem / (KB / 8), c8 = rem % (KB / 8);
+        return &vs[buf][term][r][c8 * 8];
+    };
+    floatx4 acc_h[MT][2], acc_l[MT][2];
 #pragma unroll
     for (int mt = 0; mt < MT; mt++)
 #pragma unroll
-        for (int nt = 0; nt < 4; nt++) { acc_h[mt][nt] = zero4(); acc_l[mt][nt] = zero4(); }
+        for (int nt = 0; nt < 2; nt++) { acc_h[mt][nt] = zero4(); acc_l[mt][nt] = zero4(); }
 
-    for (int64_t cb = 0; cb < a.cs; cb += KB) {
-        __syncthreads();
-        // stage 3 x ROWS x 128 bf16 (16-byte pieces)
-        for (int p = tid; p < 3 * ROWS * (KB / 8); p += 256) {
-            const int term = p / (ROWS * (KB / 8));
-            const int rem = p % (ROWS * (KB / 8));
-            const int r = rem / (KB / 8), c8 = rem % (KB / 8);
-            *reinterpret_cast<bf16x8 *>(&vs[term][r][c8 * 8]) =
-                load_bf16x8(a.vt + term * plane + (int64_t)r * a.n + c_begin + cb + c8 * 8);
+    // prologue: block 0
+    bf16x8 xa[KB / 32][2];
+    {
+        bf16x8 vt[VPT];
+#pragma unroll
+        for (int i = 0; i < VPT; i++) {
+            const int p = tid + 256 * i;
+            if (p < VPIECES) vt[i] = load_bf16x8(v_src(p, 0));
+        }
+#pragma unroll
+        for (int ks = 0; ks < KB / 32; ks++)
+#pragma unroll
+            for (int nt = 0; nt < 2; nt++) xa[ks][nt] = *reinterpret_cast<const bf16x8 *>(xrow[nt] + 32 * ks);
+#pragma unroll
+        for (int i = 0; i < VPT; i++) {
+            const int p = tid + 256 * i;
+            if (p < VPIECES) *reinterpret_cast<bf16x8 *>(v_dst(p, 0)) = vt[i];
         }
         __syncthreads();
+    }
+    for (int b = 0; b < nblk; b++) {
+        // next block (the last iteration re-requests its own block: L2 hits)
+        const int bn = b + 1 < nblk ? b + 1 : b;
+        bf16x8 vt[VPT], xn[KB / 32][2];
+#pragma unroll
+        for (int i = 0; i < VPT; i++) {
+            const int p = tid + 256 * i;
+            if (p < VPIECES) vt[i] = load_bf16x8(v_src(p, bn));
+        }
+#pragma unroll
+        for (int ks = 0; ks < KB / 32; ks++)
+#pragma unroll
+            for (int nt = 0; nt < 2; nt++)
+                xn[ks][nt] = *reinterpret_cast<const bf16x8 *>(xrow[nt] + (int64_t)bn * KB + 32 * ks);
+        __builtin_amdgcn_sched_barrier(0);
+        const int cur = b & 1;
 #pragma unroll
         for (int ks = 0; ks < KB / 32; ks++) {
-            bf16x8 b[4];
-#pragma unroll
-            for (int nt = 0; nt < 4; nt++)
-                b[nt] = *reinterpret_cast<const bf16x8 *>(xrow[nt] + cb + 32 * ks);
 #pragma unroll
             for (int mt = 0; mt < MT; mt++) {
-                const bf16x8 ah = *reinterpret_cast<const bf16x8 *>(&vs[0][16 * mt + c16][32 * ks + 8 * g]);
-                const bf16x8 am = *reinterpret_cast<const bf16x8 *>(&vs[1][16 * mt + c16][32 * ks + 8 * g]);
-                const bf16x8 al = *reinterpret_cast<const bf16x8 *>(&vs[2][16 * mt + c16][32 * ks + 8 * g]);
+                const bf16x8 ah = *reinterpret_cast<const bf16x8 *>(&vs[cur][0][16 * mt + c16][32 * ks + 8 * g]);
+                const bf16x8 am = *reinterpret_cast<const bf16x8 *>(&vs[cur][1][16 * mt + c16][32 * ks + 8 * g]);
+                const bf16x8 al = *reinterpret_cast<const bf16x8 *>(&vs[cur][2][16 * mt + c16][32 * ks + 8 * g]);
 #pragma unroll
-                for (int nt = 0; nt < 4; nt++) {
-                    acc_h[mt][nt] = mfma_bf16(ah, b[nt], acc_h[mt][nt]);
-                    acc_l[mt][nt] = mfma_bf16(am, b[nt], acc_l[mt][nt]);
-                    acc_l[mt][nt] = mfma_bf16(al, b[nt], acc_l[mt][nt]);
+                for (int nt = 0; nt < 2; nt++) {
+                    acc_h[mt][nt] = mfma_bf16(ah, xa[ks][nt], acc_h[mt][nt]);
+                    acc_l[mt][nt] = mfma_bf16(am, xa[ks][nt], acc_l[mt][nt]);
+                    acc_l[mt][nt] = mfma_bf16(al, xa[ks][nt], acc_l[mt][nt]);
                 }
             }
         }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < VPT; i++) {
+            const int p = tid + 256 * i;
+            if (p < VPIECES) *reinterpret_cast<bf16x8 *>(v_dst(p, cur ^ 1)) = vt[i];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int ks = 0; ks < KB / 32; ks++)
+#pragma unroll
+            for (int nt = 0; nt < 2; nt++) xa[ks][nt] = xn[ks][nt];
     }
 #pragma unroll
-    for (int nt = 0; nt < 4; nt++) {
-        const int64_t t = tbase + 16 * nt;
+    for (int nt = 0; nt < 2; nt++) {
+        const int64_t t = (int64_t)blockIdx.x * 128 + w * 32 + 16 * nt + c16;
         if (t >= a.T) continue;
         float *out = a.partial + t * (int64_t)a.splits * a.k + (int64_t)s * a.k;
 #pragma unroll
