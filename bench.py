@@ -32,6 +32,19 @@ METRIC = "fused NAR+INT4 quant: tokens/s and achieved HBM GB/s (% peak), 1 MI355
 HBM_PEAK_GBPS = 8000.0
 MALL_BYTES = 256 << 20
 
+# HBM bytes per call of the default (auto) path, summed over its dispatches:
+# rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE (KiB per dispatch) on bench.py,
+# FETCH_SIZE scaled by 2.0 and WRITE_SIZE by 1.0 -- the factors that make the
+# counters read a 1 GiB device copy (bench.py --copy-mb 1024) as 1 GiB each way.
+TRAFFIC_SOURCE = "profiles/hbm_traffic.md"
+TRAFFIC_BYTES = {
+    "downproj_8b": 1604.0e6,
+    "downproj_70b": 6302.1e6,
+    "qproj_3b": 171.5e6,
+    "kcache_3b": 5.8e6,
+    "vcache_decode_8b": 0.6e6,
+}
+
 
 def parse() -> argparse.Namespace:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
@@ -166,40 +179,19 @@ def main() -> int:
     ms_total = ev0.elapsed_time(ev1)
     ms_step = ms_total / args.steps
 
-    # Dominant kernel: stage B (rotate + correction + quantize).  For a full-row
-    # rank the projection (stage A) is launched separately so that B can be
-    # timed on its own with events on the same stream.
-    stage = {}
-    if full_row_rank:
-        splits = 8 if prepared is not None else 1
-        partial = torch.empty((w.tokens, splits * w.k), dtype=torch.float32, device=dev)
-        ea = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
-        ta, tb = [], []
-        for i in range(args.warmup + args.steps):
-            c, s, z = outs[i % R]
-            ea[0].record(stream)
-            ops.rank_projection(xs[i % R], v, partial, rank_mode=mode, prepared=prepared)
-            ea[1].record(stream)
-            ops.rotate_quant(xs[i % R], hadamard=w.hadamard, v=v, w_t=wt, prepared=prepared, partial=partial,
-                             group=w.group, codes=c, scales=s, zeros=z, rank_mode=mode)
-            ea[2].record(stream)
-            torch.cuda.synchronize(dev)
-            if i >= args.warmup:
-                ta.append(ea[0].elapsed_time(ea[1]))
-                tb.append(ea[1].elapsed_time(ea[2]))
-        stage = {"projection_ms": statistics.mean(ta), "transform_quant_ms": statistics.mean(tb)}
-        dom_ms = stage["transform_quant_ms"]
-        dom_name = "transform_quant (FWHT, Paley, rank-k correction, INT4)"
-        factor_b = w.w_t.nbytes
-    else:
-        dom_ms = ms_step
-        dom_name = "rotate_quant (single fused kernel)"
-        factor_b = 0 if w.v is None else w.v.nbytes + w.w_t.nbytes
-
+    # Roofline of the operator call.  One call is one dispatch sequence on the
+    # current stream (full-row rank: proj_mfma -> kron_mfma / rq_seg -> fold_u
+    # -> corr_quant; otherwise one rq_seg / kron dispatch), so the per-launch
+    # duration is ms_step, HIP-event timed above on that stream.  Algorithmic
+    # bytes: T*(2n + n/2 + 4n/b) + factor bytes.  Traffic: HBM bytes per call
+    # measured with rocprofv3 (FETCH_SIZE x2 + WRITE_SIZE, copy-calibrated).
     t, n, b = w.tokens, w.n, w.group
     alg_bytes = w.algorithmic_bytes()
-    dom_bytes = t * (2 * n + n // 2 + 4 * n // b) + factor_b
-    achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
+    achieved = alg_bytes / (ms_step * 1e-3) / 1e9
+    kernels = ("proj_mfma + kron_mfma + fold_u + corr_quant" if full_row_rank and w.hadamard[0] > 1 and
+               mode != ops.RANK_EXACT else "rq_seg" if w.hadamard[0] == 1 and not full_row_rank else
+               "rotate_quant dispatch sequence")
+    traffic = TRAFFIC_BYTES.get(args.config) if mode == ops.RANK_AUTO else None
     line = {
         "metric": METRIC,
         "value": t / (ms_step * 1e-3),
@@ -218,9 +210,9 @@ def main() -> int:
         "achieved_gbps": alg_bytes / (ms_step * 1e-3) / 1e9,
         "hbm_frac": alg_bytes / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBPS,
         "wall_s": wall,
-        "stages_ms": stage,
-        "roofline": {"kernel": dom_name, "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS,
-                     "unit": "GB/s", "frac": achieved / HBM_PEAK_GBPS, "traffic": None},
+        "roofline": {"kernel": f"rotate_quant call ({kernels})", "bound": "hbm", "achieved": achieved,
+                     "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBPS,
+                     "traffic": traffic, "traffic_source": TRAFFIC_SOURCE if traffic else None},
     }
     if w.dest_rows is not None:
         line["us_per_call"] = ms_step * 1e3

@@ -177,16 +177,43 @@ int launch_row_mqb(const RowArgs &a, hipStream_t s)
     return check_launch("rq_row_kernel");
 }
 
+// Grid of a persistent kernel: as many workgroups as fit on the device at
+// once (occupancy at this block size and LDS), at most `work`.  Cached per
+// kernel and device.
+template <typename K>
+int64_t persistent_grid(K kernel, int threads, size_t lds, int64_t work)
+{
+    static thread_local int cached_dev = -1;
+    static thread_local int64_t cached = 0;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+    if (dev != cached_dev) {
+        int cus = 0, per = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1) cus = 256;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, reinterpret_cast<const void *>(kernel), threads, lds) !=
+                hipSuccess || per < 1)
+            per = 1;
+        cached = (int64_t)cus * per;
+        cached_dev = dev;
+    }
+    return cached < work ? cached : work;
+}
+
 template <int M, int Q, int B>
 int launch_kron_mqb(const KronArgs &a, bool quant, hipStream_t s)
 {
     const size_t lds = sizeof(float) * M * (Q + KPAD);
+    constexpr bool persist = Q >= 1024;   // 115 KB of LDS: one workgroup per CU
     if (quant) {
-        if (int rc = set_lds(&kron_mfma_kernel<M, Q, B, true>, lds)) return rc;
-        hipLaunchKernelGGL((kron_mfma_kernel<M, Q, B, true>), dim3((unsigned)a.T), dim3(16 * M), lds, s, a);
+        auto k = &kron_mfma_kernel<M, Q, B, true, persist>;
+        if (int rc = set_lds(k, lds)) return rc;
+        const int64_t grid = persist ? persistent_grid(k, 16 * M, lds, a.T) : a.T;
+        hipLaunchKernelGGL((kron_mfma_kernel<M, Q, B, true, persist>), dim3((unsigned)grid), dim3(16 * M), lds, s, a);
     } else {
-        if (int rc = set_lds(&kron_mfma_kernel<M, Q, 128, false>, lds)) return rc;
-        hipLaunchKernelGGL((kron_mfma_kernel<M, Q, 128, false>), dim3((unsigned)a.T), dim3(16 * M), lds, s, a);
+        auto k = &kron_mfma_kernel<M, Q, 128, false, persist>;
+        if (int rc = set_lds(k, lds)) return rc;
+        const int64_t grid = persist ? persistent_grid(k, 16 * M, lds, a.T) : a.T;
+        hipLaunchKernelGGL((kron_mfma_kernel<M, Q, 128, false, persist>), dim3((unsigned)grid), dim3(16 * M), lds, s, a);
     }
     return check_launch("kron_mfma_kernel");
 }

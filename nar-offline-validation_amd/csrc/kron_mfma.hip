@@ -1,6 +1,6 @@
 // Kronecker row transform with the Paley factor on bf16 MFMA.
 //
-// One workgroup per token, one 16-lane row per segment (16 M threads):
+// Persistent workgroups over tokens, one 16-lane row per segment (16 M threads):
 //   phase 1  F[a, :] = FWHT_Q(x[a*Q:(a+1)*Q]) / fp32(sqrt(Q))   (DPP, as rq_row.hip)
 //   phase 2  P[a, c] = hm * S[a, c],  S = Hm(+-1) F                  (MFMA)
 //            F enters as three exact bf16 terms; S1 = Hm F_hi and S23 = Hm (F_mid + F_lo)
@@ -32,7 +32,10 @@ struct KronArgs {
 // phase 2 (lanes of a wave read rows 8 apart) fall in different banks.
 constexpr int KPAD = 4;
 
-template <int M, int Q, int B, bool QUANT>
+// PERSIST: a grid of at most one wave of workgroups walks all tokens,
+// prefetching the next token's x (pays where LDS allows one workgroup per CU);
+// otherwise one workgroup per token.
+template <int M, int Q, int B, bool QUANT, bool PERSIST>
 __global__ void __launch_bounds__(16 * M)
 kron_mfma_kernel(KronArgs a)
 {
@@ -48,30 +51,49 @@ kron_mfma_kernel(KronArgs a)
     const int l16 = tid & 15;
     const int row = tid >> 4;
     const int chunk = lane_chunk(l16);
-    const int64_t t = blockIdx.x;
-    const uint16_t *xt = a.x + t * a.ldx;
 
-    // Paley rows as the MFMA A operand (issued first; used after phase 1)
+    // Paley rows as the MFMA A operand
     const int lane = tid & 63, wv = tid >> 6;
     const int g = lane >> 4, c16 = lane & 15;
-    uint32_t negbits[NMT];
+    bf16x8 ha[NMT];
 #pragma unroll
     for (int mt = 0; mt < NMT; mt++) {
         const int r = 16 * mt + c16;
-        negbits[mt] = r < M ? a.paley.neg[r] : 0u;
+        const uint32_t negbits = r < M ? a.paley.neg[r] : 0u;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int c = 8 * g + j;
+            float e = 0.0f;
+            if (r < M && c < M) e = ((negbits >> c) & 1u) ? -1.0f : 1.0f;
+            ha[mt][j] = (__bf16)e;
+        }
     }
 
+    // Persistent over tokens t = blockIdx.x, + gridDim.x, ...; the next token's
+    // x segment is requested before the current one is transformed.
+    int64_t t = blockIdx.x;
+    if (t >= a.T) return;
+    const int s = row;
+    uint4 xw[NH];
+#pragma unroll
+    for (int h = 0; h < NH; h++)
+        xw[h] = *reinterpret_cast<const uint4 *>(a.x + t * a.ldx + s * Q + h * 128 + chunk * 8);
+    for (; t < a.T; t += gridDim.x) {
     // ---- phase 1 (identical arithmetic to rq_row_kernel): row `row` transforms segment `row`
     {
-        const int s = row;
         float v[NV];
 #pragma unroll
         for (int h = 0; h < NH; h++) {
-            uint4 xw = *reinterpret_cast<const uint4 *>(xt + s * Q + h * 128 + chunk * 8);
-            v[h * 8 + 0] = bf16lo(xw.x); v[h * 8 + 1] = bf16hi(xw.x);
-            v[h * 8 + 2] = bf16lo(xw.y); v[h * 8 + 3] = bf16hi(xw.y);
-            v[h * 8 + 4] = bf16lo(xw.z); v[h * 8 + 5] = bf16hi(xw.z);
-            v[h * 8 + 6] = bf16lo(xw.w); v[h * 8 + 7] = bf16hi(xw.w);
+            v[h * 8 + 0] = bf16lo(xw[h].x); v[h * 8 + 1] = bf16hi(xw[h].x);
+            v[h * 8 + 2] = bf16lo(xw[h].y); v[h * 8 + 3] = bf16hi(xw[h].y);
+            v[h * 8 + 4] = bf16lo(xw[h].z); v[h * 8 + 5] = bf16hi(xw[h].z);
+            v[h * 8 + 6] = bf16lo(xw[h].w); v[h * 8 + 7] = bf16hi(xw[h].w);
+        }
+        if constexpr (PERSIST) {
+            const int64_t tn = t + gridDim.x < a.T ? t + gridDim.x : a.T - 1;
+#pragma unroll
+            for (int h = 0; h < NH; h++)
+                xw[h] = *reinterpret_cast<const uint4 *>(a.x + tn * a.ldx + s * Q + h * 128 + chunk * 8);
         }
         if (a.signs) {
 #pragma unroll
@@ -127,17 +149,6 @@ kron_mfma_kernel(KronArgs a)
 
     // ---- phase 2: Paley product on MFMA, one 16-column block at a time, in place
     {
-        bf16x8 ha[NMT];
-#pragma unroll
-        for (int mt = 0; mt < NMT; mt++) {
-#pragma unroll
-            for (int j = 0; j < 8; j++) {
-                const int c = 8 * g + j;
-                float e = 0.0f;
-                if (16 * mt + c16 < M && c < M) e = ((negbits[mt] >> c) & 1u) ? -1.0f : 1.0f;
-                ha[mt][j] = (__bf16)e;
-            }
-        }
         const float hm = a.hm;
         constexpr int CB = Q / 16;
         for (int cb = wv; cb < CB; cb += NW) {
@@ -170,7 +181,6 @@ kron_mfma_kernel(KronArgs a)
     if constexpr (!QUANT) {
         float4 *dst = reinterpret_cast<float4 *>(a.P + t * N);
         for (int i = tid; i < N / 4; i += NT) dst[i] = *reinterpret_cast<const float4 *>(F + fidx(i));
-        return;
     } else {
         if (a.rotated) {
             for (int i = tid; i < N / 4; i += NT)
@@ -205,6 +215,9 @@ kron_mfma_kernel(KronArgs a)
                 }
             }
         }
+    }
+    if constexpr (!PERSIST) break;
+    __syncthreads();   // F is rewritten by the next token
     }
 }
 
