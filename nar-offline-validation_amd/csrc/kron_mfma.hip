@@ -46,7 +46,7 @@ kron_mfma_kernel(KronArgs a)
     constexpr int NMT = (M + 15) / 16;
     constexpr int NT = 16 * M;              // threads: one 16-lane row per segment
     constexpr int NW = NT / 64;             // waves
-    extern __shared__ float F[];
+    extern __shared__ __align__(16) float F[];
     const int tid = threadIdx.x;
     const int l16 = tid & 15;
     const int row = tid >> 4;
@@ -160,7 +160,7 @@ kron_mfma_kernel(KronArgs a)
                 f[j] = ar < M ? F[ar * QS + c] : 0.0f;
             }
             bf16x8 bh, bm, bl;
-            split3x8(f, bh, bm, bl);
+            split3x8_trunc(f, bh, bm, bl);
 #pragma unroll
             for (int mt = 0; mt < NMT; mt++) {
                 const floatx4 s1 = mfma_bf16(ha[mt], bh, zero4());
@@ -176,15 +176,16 @@ kron_mfma_kernel(KronArgs a)
     }
     __syncthreads();
 
-    // row-major float4 index i of the token's N floats -> its place in F
-    auto fidx = [](int i) { return (i / (Q / 4)) * QS + (i % (Q / 4)) * 4; };
+    // row-major float4 index i of the token's N floats -> its float4 in F
+    const float4 *F4 = reinterpret_cast<const float4 *>(F);
+    auto f4 = [](int i) { return (i / (Q / 4)) * (QS / 4) + (i % (Q / 4)); };
     if constexpr (!QUANT) {
         float4 *dst = reinterpret_cast<float4 *>(a.P + t * N);
-        for (int i = tid; i < N / 4; i += NT) dst[i] = *reinterpret_cast<const float4 *>(F + fidx(i));
+        for (int i = tid; i < N / 4; i += NT) dst[i] = F4[f4(i)];
     } else {
         if (a.rotated) {
             for (int i = tid; i < N / 4; i += NT)
-                reinterpret_cast<float4 *>(a.rotated + t * N)[i] = *reinterpret_cast<const float4 *>(F + fidx(i));
+                reinterpret_cast<float4 *>(a.rotated + t * N)[i] = F4[f4(i)];
         }
         constexpr int G8 = B / 8;
         constexpr int CHUNKS = N / 8;
@@ -195,8 +196,7 @@ kron_mfma_kernel(KronArgs a)
             const int chs = ok ? ch : 0;
             float v[8];
             {
-                const float4 *s = reinterpret_cast<const float4 *>(F + fidx(2 * chs));
-                float4 p0 = s[0], p1 = s[1];
+                const float4 p0 = F4[f4(2 * chs)], p1 = F4[f4(2 * chs) + 1];
                 v[0] = p0.x; v[1] = p0.y; v[2] = p0.z; v[3] = p0.w;
                 v[4] = p1.x; v[5] = p1.y; v[6] = p1.z; v[7] = p1.w;
             }

@@ -52,6 +52,32 @@ __device__ __forceinline__ void split3x8(const float (&x)[8], bf16x8 &h, bf16x8 
     }
 }
 
+// The same decomposition by truncation, for eight values at once: h is x with
+// the low 16 bits cleared (a bf16 value), r = x - h is exact, m is r with its
+// low 16 bits cleared, l = r - m is exact and has at most 8 significant bits,
+// so the upper halves of h, m and l are the three bf16 terms.  Packing takes
+// the upper halves of two fp32 words per v_perm_b32.
+__device__ __forceinline__ void split3x8_trunc(const float (&x)[8], bf16x8 &h, bf16x8 &m, bf16x8 &l)
+{
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    u32x4 hw, mw, lw;
+#pragma unroll
+    for (int d = 0; d < 4; d++) {
+        const uint32_t ua = __float_as_uint(x[2 * d]), ub = __float_as_uint(x[2 * d + 1]);
+        const float ra = x[2 * d] - __uint_as_float(ua & 0xffff0000u);
+        const float rb = x[2 * d + 1] - __uint_as_float(ub & 0xffff0000u);
+        const uint32_t ura = __float_as_uint(ra), urb = __float_as_uint(rb);
+        const float la = ra - __uint_as_float(ura & 0xffff0000u);
+        const float lb = rb - __uint_as_float(urb & 0xffff0000u);
+        hw[d] = __builtin_amdgcn_perm(ub, ua, 0x07060302u);
+        mw[d] = __builtin_amdgcn_perm(urb, ura, 0x07060302u);
+        lw[d] = __builtin_amdgcn_perm(__float_as_uint(lb), __float_as_uint(la), 0x07060302u);
+    }
+    h = __builtin_bit_cast(bf16x8, hw);
+    m = __builtin_bit_cast(bf16x8, mw);
+    l = __builtin_bit_cast(bf16x8, lw);
+}
+
 __device__ __forceinline__ bf16x8 load_bf16x8(const __bf16 *p)
 {
     return *reinterpret_cast<const bf16x8 *>(p);
