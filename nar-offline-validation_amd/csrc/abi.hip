@@ -357,7 +357,9 @@ int launch_corr_quant(CorrQuantArgs a, int b, hipStream_t s)
 {
     if (a.T == 0) return NARHIP_OK;
     const int ks = a.kp / 32;
-    const int cw = (ks == 1 && a.n % 256 == 0) ? 256 : 128;
+    // 256 channels (48 KB of W^T terms) per workgroup where the register tile
+    // of two groups fits (b <= 64, k <= 32); else one 128-channel block
+    const int cw = (ks == 1 && b <= 64 && a.n % 256 == 0) ? 256 : 128;
     if (a.n % cw || cw % b) return fail(NARHIP_EUNSUPPORTED, "rank correction needs n %% 128 == 0");
     a.ncb = a.n / cw;
     const int64_t tiles = (a.T + 127) / 128;

@@ -235,73 +235,85 @@ __device__ __forceinline__ void cq_load(CqUnit<B> &p, const float *prow)
     }
 }
 
-// x' = P - u W^T for one unit (W^T terms of the group at wl in LDS, planes of
-// WPLANE elements), then its codes, scales and zeros, staged in LDS: codes of
-// token c16 at crow[c16 * CSTRIDE + ...] (uint16 = four codes), scale and zero
-// at sz[2 c16], sz[2 c16 + 1].  Only x' (variant ROT) goes to memory here.
-template <int B, int KS, int WPLANE, int CSTRIDE, bool ROT>
-__device__ __forceinline__ void cq_unit(CqUnit<B> &xt, const CorrQuantArgs &a, const bf16x8 (&ub)[3][KS],
-                                        float *rrow, const __bf16 *wl, uint16_t *crow, uint16_t *sz, int lane)
+// x' = P - u W^T for one group of B channels and both 16-token halves (W^T
+// terms of the group at wl in LDS: rows of WROW bf16, planes of WPLANE; each
+// fragment read once and used for both halves), then codes, scales and zeros
+// staged in LDS: codes of token 16h + c16 at crow[(16h + c16) * CSTRIDE + ...]
+// (uint16 = four codes), scale and zero at sz[2 (16h + c16)], sz[... + 1].
+// Only x' (variant ROT) goes to memory here.
+template <int B, int KS, int WROW, int WPLANE, int CSTRIDE, bool ROT>
+__device__ __forceinline__ void cq_group(CqUnit<B> (&xt)[2], const CorrQuantArgs &a,
+                                         const bf16x8 (&ub)[2][3][KS], float *const (&rrow)[2],
+                                         const __bf16 *wl, uint16_t *crow, uint16_t *sz, int lane)
 {
-    constexpr int KP = 32 * KS;
     constexpr int MTG = B / 16;
     const int g = lane >> 4, c16 = lane & 15;
-    auto &xv = xt.v;
 #pragma unroll
     for (int mt = 0; mt < MTG; mt++) {
-        const __bf16 *wrow = wl + (16 * mt + c16) * KP + 8 * g;
-        floatx4 main = zero4(), small = zero4();
+        const __bf16 *wrow = wl + (16 * mt + c16) * WROW + 8 * g;
+        bf16x8 wh[KS], wm[KS], wo[KS];
 #pragma unroll
         for (int ks = 0; ks < KS; ks++) {
-            const bf16x8 wh = *reinterpret_cast<const bf16x8 *>(wrow + 32 * ks);
-            const bf16x8 wm = *reinterpret_cast<const bf16x8 *>(wrow + WPLANE + 32 * ks);
-            const bf16x8 wo = *reinterpret_cast<const bf16x8 *>(wrow + 2 * WPLANE + 32 * ks);
-            main = mfma_bf16(wh, ub[0][ks], main);
-            small = mfma_bf16(wm, ub[0][ks], small);
-            small = mfma_bf16(wh, ub[1][ks], small);
-            small = mfma_bf16(wo, ub[0][ks], small);
-            small = mfma_bf16(wh, ub[2][ks], small);
-            small = mfma_bf16(wm, ub[1][ks], small);
+            wh[ks] = *reinterpret_cast<const bf16x8 *>(wrow + 32 * ks);
+            wm[ks] = *reinterpret_cast<const bf16x8 *>(wrow + WPLANE + 32 * ks);
+            wo[ks] = *reinterpret_cast<const bf16x8 *>(wrow + 2 * WPLANE + 32 * ks);
         }
 #pragma unroll
-        for (int i = 0; i < 4; i++) xv[mt][i] = xv[mt][i] - (main[i] + small[i]);
+        for (int h = 0; h < 2; h++) {
+            floatx4 main = zero4(), small = zero4();
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++) {
+                main = mfma_bf16(wh[ks], ub[h][0][ks], main);
+                small = mfma_bf16(wm[ks], ub[h][0][ks], small);
+                small = mfma_bf16(wh[ks], ub[h][1][ks], small);
+                small = mfma_bf16(wo[ks], ub[h][0][ks], small);
+                small = mfma_bf16(wh[ks], ub[h][2][ks], small);
+                small = mfma_bf16(wm[ks], ub[h][1][ks], small);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++) xt[h].v[mt][i] = xt[h].v[mt][i] - (main[i] + small[i]);
+        }
     }
-    if constexpr (ROT) {
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        auto &xv = xt[h].v;
+        if constexpr (ROT) {
+#pragma unroll
+            for (int mt = 0; mt < MTG; mt++)
+                *reinterpret_cast<float4 *>(rrow[h] + 16 * mt) = make_float4(xv[mt][0], xv[mt][1], xv[mt][2], xv[mt][3]);
+        }
+        // the group of token c16 is spread over lanes c16 + 16g
+        float lo = xv[0][0], hi = lo;
 #pragma unroll
         for (int mt = 0; mt < MTG; mt++)
-            *reinterpret_cast<float4 *>(rrow + 16 * mt) = make_float4(xv[mt][0], xv[mt][1], xv[mt][2], xv[mt][3]);
-    }
-    // the group of token c16 is spread over lanes c16 + 16g
-    float lo = xv[0][0], hi = lo;
 #pragma unroll
-    for (int mt = 0; mt < MTG; mt++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) { lo = fminf(lo, xv[mt][i]); hi = fmaxf(hi, xv[mt][i]); }
-    lo = fminf(lo, __shfl_xor(lo, 16)); hi = fmaxf(hi, __shfl_xor(hi, 16));
-    lo = fminf(lo, __shfl_xor(lo, 32)); hi = fmaxf(hi, __shfl_xor(hi, 32));
-    const GroupParams gp = group_params(lo, hi);
-    const float rs = 1.0f / gp.s;
-    bool tie = false;
-    uint32_t q16[MTG];
-#pragma unroll
-    for (int mt = 0; mt < MTG; mt++) {
-        q16[mt] = 0;
-#pragma unroll
-        for (int i = 0; i < 4; i++) q16[mt] |= quant_code_fast(xv[mt][i], gp.z, rs, tie) << (4 * i);
-    }
-    if (__builtin_expect(__any(tie), 0)) {
+            for (int i = 0; i < 4; i++) { lo = fminf(lo, xv[mt][i]); hi = fmaxf(hi, xv[mt][i]); }
+        lo = fminf(lo, __shfl_xor(lo, 16)); hi = fmaxf(hi, __shfl_xor(hi, 16));
+        lo = fminf(lo, __shfl_xor(lo, 32)); hi = fmaxf(hi, __shfl_xor(hi, 32));
+        const GroupParams gp = group_params(lo, hi);
+        const float rs = 1.0f / gp.s;
+        bool tie = false;
+        uint32_t q16[MTG];
 #pragma unroll
         for (int mt = 0; mt < MTG; mt++) {
             q16[mt] = 0;
 #pragma unroll
-            for (int i = 0; i < 4; i++) q16[mt] |= quant_code(xv[mt][i], gp) << (4 * i);
+            for (int i = 0; i < 4; i++) q16[mt] |= quant_code_fast(xv[mt][i], gp.z, rs, tie) << (4 * i);
         }
-    }
+        if (__builtin_expect(__any(tie), 0)) {
 #pragma unroll
-    for (int mt = 0; mt < MTG; mt++) crow[c16 * CSTRIDE + 4 * mt + g] = (uint16_t)q16[mt];
-    if (g == 0) {
-        sz[2 * c16] = gp.s16;
-        sz[2 * c16 + 1] = gp.z16;
+            for (int mt = 0; mt < MTG; mt++) {
+                q16[mt] = 0;
+#pragma unroll
+                for (int i = 0; i < 4; i++) q16[mt] |= quant_code(xv[mt][i], gp) << (4 * i);
+            }
+        }
+#pragma unroll
+        for (int mt = 0; mt < MTG; mt++) crow[(16 * h + c16) * CSTRIDE + 4 * mt + g] = (uint16_t)q16[mt];
+        if (g == 0) {
+            sz[2 * (16 * h + c16)] = gp.s16;
+            sz[2 * (16 * h + c16) + 1] = gp.z16;
+        }
     }
 }
 
@@ -309,9 +321,8 @@ __device__ __forceinline__ void cq_unit(CqUnit<B> &xt, const CorrQuantArgs &a, c
 // channels: it stages their W^T terms in LDS once ([3][CW][KP], 48 KB) and
 // then runs a.tpw tiles of 128 tokens over them.  Within a tile every wave
 // works alone (no further workgroup barriers) on 32 tokens x CW channels:
-// all of its P (128 VGPRs at CW = 256) is requested at once, then the units
-// (group gi, 16-token half h) are processed in load order, each waiting only
-// for its own loads.  Codes, scales and zeros are staged in LDS and stored
+// all of its P (128 VGPRs at CW = 256) is requested at once, then the groups
+// are processed in load order, each waiting only for its own loads.  Codes, scales and zeros are staged in LDS and stored
 // after the last unit; tokens >= T store into a scratch row, so that no
 // memory operation sits under a branch and the wait counts stay exact.
 // Workgroups are dispatched to the 8 XCDs round-robin by block id, so the
@@ -323,9 +334,10 @@ __global__ void __launch_bounds__(256, 2)
 corr_quant_kernel(CorrQuantArgs a)
 {
     constexpr int KP = 32 * KS;
-    constexpr int WPLANE = CW * KP;
+    constexpr int WROW = KP + 8;             // padded channel row: fragment reads hit distinct banks
+    constexpr int WPLANE = CW * WROW;
     constexpr int NG = CW / B;               // groups per channel block
-    constexpr int CSTRIDE = CW / 4 + 8;      // uint16 per token row of staged codes (16-byte rows)
+    constexpr int CSTRIDE = CW / 4;          // uint16 per token row of staged codes (16-byte rows)
     __shared__ __align__(16) __bf16 ws[3 * WPLANE];
     __shared__ __align__(16) uint16_t cst[4][32 * CSTRIDE];
     __shared__ __align__(16) uint16_t szs[4][NG][64];   // [2 t + 0] scale, [2 t + 1] zero of token t
@@ -339,10 +351,11 @@ corr_quant_kernel(CorrQuantArgs a)
     const int64_t cbeg = cb * CW;
     const int64_t plane = (int64_t)KP * a.n;
 
-    for (int p = tid; p < 3 * WPLANE / 8; p += 256) {
-        const int term = p / (WPLANE / 8), rem = p % (WPLANE / 8);
-        *reinterpret_cast<bf16x8 *>(&ws[term * WPLANE + rem * 8]) =
-            load_bf16x8(a.wtt + term * plane + cbeg * KP + rem * 8);
+    for (int p = tid; p < 3 * CW * (KP / 8); p += 256) {
+        const int term = p / (CW * (KP / 8)), rem = p % (CW * (KP / 8));
+        const int ch = rem / (KP / 8), k8 = rem % (KP / 8);
+        *reinterpret_cast<bf16x8 *>(&ws[term * WPLANE + ch * WROW + k8 * 8]) =
+            load_bf16x8(a.wtt + term * plane + (cbeg + ch) * KP + k8 * 8);
     }
     __syncthreads();
 
@@ -379,14 +392,12 @@ corr_quant_kernel(CorrQuantArgs a)
             for (int h = 0; h < 2; h++) cq_load<B>(U[gi][h], prow[h] + gi * B);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int gi = 0; gi < NG; gi++)
-#pragma unroll
-            for (int h = 0; h < 2; h++) {
-                cq_unit<B, KS, WPLANE, CSTRIDE, ROT>(U[gi][h], a, ub[h], ROT ? rrow[h] + gi * B : nullptr,
-                                                     ws + gi * B * KP, &cst[w][16 * h * CSTRIDE + gi * B / 4],
-                                                     &szs[w][gi][32 * h], lane);
-                __builtin_amdgcn_sched_barrier(0);
-            }
+        for (int gi = 0; gi < NG; gi++) {
+            float *const rr[2] = {ROT ? rrow[0] + gi * B : nullptr, ROT ? rrow[1] + gi * B : nullptr};
+            cq_group<B, KS, WROW, WPLANE, CSTRIDE, ROT>(U[gi], a, ub, rr, ws + gi * B * WROW,
+                                                        &cst[w][gi * B / 4], &szs[w][gi][0], lane);
+            __builtin_amdgcn_sched_barrier(0);
+        }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
