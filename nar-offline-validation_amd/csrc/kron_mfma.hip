@@ -28,9 +28,14 @@ struct KronArgs {
     float sq, rsq, hm;     // fp32(sqrt(Q)), RN(1/sq), RN(1/fp32(sqrt(M)))
 };
 
-// Rows of F in LDS are padded by KPAD floats, so that the column accesses of
-// phase 2 (lanes of a wave read rows 8 apart) fall in different banks.
-constexpr int KPAD = 4;
+// F in LDS: row a of the token's M x Q block at a * Q, column c stored at
+// c ^ fsw(a).  Phase 2 reads a column from rows 8g + j and writes rows
+// 16 mt + 4g + i (g = lane / 16); flipping column bit 4 by bit 3 ^ bit 2 of the
+// row puts lanes with g = 0 and g = 1 in different halves of the 32 banks in
+// both, and moves only whole 16-float blocks, so the row-wise float4 accesses of
+// phases 1 and 3 stay aligned.
+constexpr int KPAD = 0;
+__device__ __forceinline__ int fsw(int a) { return (((a >> 3) ^ (a >> 2)) & 1) << 4; }
 
 // PERSIST: a grid of at most one wave of workgroups walks all tokens,
 // prefetching the next token's x (pays where LDS allows one workgroup per CU);
@@ -42,7 +47,7 @@ kron_mfma_kernel(KronArgs a)
     constexpr int NH = Q / 128;
     constexpr int NV = 8 * NH;
     constexpr int N = M * Q;
-    constexpr int QS = Q + KPAD;            // LDS row stride (floats)
+    constexpr int QS = Q + KPAD;            // LDS row stride (floats, no padding)
     constexpr int NMT = (M + 15) / 16;
     constexpr int NT = 16 * M;              // threads: one 16-lane row per segment
     constexpr int NW = NT / 64;             // waves
@@ -140,7 +145,7 @@ kron_mfma_kernel(KronArgs a)
         div_sqrt_q<Q>(v, a.sq, a.rsq);
 #pragma unroll
         for (int h = 0; h < NH; h++) {
-            float4 *d = reinterpret_cast<float4 *>(F + s * QS + h * 128 + chunk * 8);
+            float4 *d = reinterpret_cast<float4 *>(F + s * QS + ((h * 128 + chunk * 8) ^ fsw(s)));
             d[0] = make_float4(v[h * 8 + 0], v[h * 8 + 1], v[h * 8 + 2], v[h * 8 + 3]);
             d[1] = make_float4(v[h * 8 + 4], v[h * 8 + 5], v[h * 8 + 6], v[h * 8 + 7]);
         }
@@ -157,7 +162,7 @@ kron_mfma_kernel(KronArgs a)
 #pragma unroll
             for (int j = 0; j < 8; j++) {
                 const int ar = 8 * g + j;
-                f[j] = ar < M ? F[ar * QS + c] : 0.0f;
+                f[j] = ar < M ? F[ar * QS + (c ^ fsw(ar))] : 0.0f;
             }
             bf16x8 bh, bm, bl;
             split3x8_trunc(f, bh, bm, bl);
@@ -169,7 +174,7 @@ kron_mfma_kernel(KronArgs a)
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     const int ar = 16 * mt + 4 * g + i;
-                    if (ar < M) F[ar * QS + c] = __builtin_fmaf(hm, s1[i], hm * s2[i]);
+                    if (ar < M) F[ar * QS + (c ^ fsw(ar))] = __builtin_fmaf(hm, s1[i], hm * s2[i]);
                 }
             }
         }
@@ -178,7 +183,10 @@ kron_mfma_kernel(KronArgs a)
 
     // row-major float4 index i of the token's N floats -> its float4 in F
     const float4 *F4 = reinterpret_cast<const float4 *>(F);
-    auto f4 = [](int i) { return (i / (Q / 4)) * (QS / 4) + (i % (Q / 4)); };
+    auto f4 = [](int i) {
+        const int a = i / (Q / 4);
+        return a * (QS / 4) + ((i % (Q / 4)) ^ (fsw(a) >> 2));
+    };
     if constexpr (!QUANT) {
         float4 *dst = reinterpret_cast<float4 *>(a.P + t * N);
         for (int i = tid; i < N / 4; i += NT) dst[i] = F4[f4(i)];

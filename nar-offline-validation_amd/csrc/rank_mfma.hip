@@ -337,7 +337,8 @@ corr_quant_kernel(CorrQuantArgs a)
     constexpr int WROW = KP + 8;             // padded channel row: fragment reads hit distinct banks
     constexpr int WPLANE = CW * WROW;
     constexpr int NG = CW / B;               // groups per channel block
-    constexpr int CSTRIDE = CW / 4;          // uint16 per token row of staged codes (16-byte rows)
+    constexpr int CSTRIDE = CW / 4 + 8;      // uint16 per token row of staged codes (16-byte rows, padded
+                                             // so the 16 tokens of a store land in different banks)
     __shared__ __align__(16) __bf16 ws[3 * WPLANE];
     __shared__ __align__(16) uint16_t cst[4][32 * CSTRIDE];
     __shared__ __align__(16) uint16_t szs[4][NG][64];   // [2 t + 0] scale, [2 t + 1] zero of token t
