@@ -60,14 +60,15 @@ struct ProjMfmaArgs {
 
 // grid (ceil(T/128), splits), block 256.  Wave w owns tokens 32w..32w+31 of
 // the 128-token tile as two 16-token N tiles; all MT rank tiles of 16 rows.
-// The split's channels are walked in blocks of 128 (64 for k > 32): the V
-// terms of a block are staged in LDS (two buffers, one barrier per block) and
-// x of the next block is requested while the current block's MFMAs run.
+// The split's channels are walked in blocks of 64: the V terms of a block are
+// staged in LDS (two buffers, one barrier per block) and x of the next block is
+// requested while the current block's MFMAs run.
 template <int MT>
 __global__ void __launch_bounds__(256, 2)
 proj_mfma_kernel(ProjMfmaArgs a)
 {
-    constexpr int KB = MT <= 2 ? 128 : 64;  // channels per block (LDS: two buffers)
+    constexpr int KB = 64;                  // channels per block (two LDS buffers, 28 KB at k = 32:
+                                            // leaves room for a concurrent transform workgroup)
     constexpr int ROWS = 16 * MT;
     constexpr int VSTR = KB + 8;            // padded LDS row (bf16)
     constexpr int VPIECES = 3 * ROWS * (KB / 8);              // 16-byte pieces per block
