@@ -52,7 +52,8 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="downproj_8b",
-                    choices=["kcache_3b", "qproj_3b", "downproj_8b", "vcache_decode_8b", "downproj_70b"])
+                    choices=["kcache_3b", "qproj_3b", "downproj_8b", "vcache_decode_8b", "downproj_70b",
+                             "e17_8b_k8", "e17_8b_k32", "e17_3b_k8", "e17_3b_k32"])
     ap.add_argument("--rank-mode", default="auto", choices=["auto", "exact", "mfma"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU baseline work")
@@ -142,7 +143,7 @@ def main() -> int:
     from narhip import ops, workloads
 
     mode = {"auto": ops.RANK_AUTO, "exact": ops.RANK_EXACT, "mfma": ops.RANK_MFMA}[args.rank_mode]
-    w = workloads.CONFIGS[args.config]()
+    w = (workloads.CONFIGS.get(args.config) or workloads.REFERENCE_SETTINGS[args.config])()
     dev = torch.device("cuda:0")
     x_host = torch.from_numpy(w.x.view(np.int16))
     in_bytes = w.x.nbytes
@@ -188,9 +189,13 @@ def main() -> int:
     t, n, b = w.tokens, w.n, w.group
     alg_bytes = w.algorithmic_bytes()
     achieved = alg_bytes / (ms_step * 1e-3) / 1e9
-    kernels = ("proj_mfma + kron_mfma + fold_u + corr_quant" if full_row_rank and w.hadamard[0] > 1 and
-               mode != ops.RANK_EXACT else "rq_seg" if w.hadamard[0] == 1 and not full_row_rank else
-               "rotate_quant dispatch sequence")
+    kron = w.hadamard[0] > 1
+    if full_row_rank and mode != ops.RANK_EXACT and (w.k >= 16 or mode == ops.RANK_MFMA):
+        kernels = f"proj_mfma + {'kron_mfma' if kron else 'rq_seg'} + fold_u + corr_quant"
+    elif full_row_rank:
+        kernels = "proj_exact + corr_exact + rq_row" if kron else "proj_exact + rq_seg"
+    else:
+        kernels = "kron_mfma" if kron else "rq_seg"
     traffic = TRAFFIC_BYTES.get(args.config) if mode == ops.RANK_AUTO else None
     line = {
         "metric": METRIC,

@@ -139,7 +139,10 @@ int launch_seg_qb(const SegArgs &a, int mode, hipStream_t s)
     switch (mode) {
     case RANK_NONE: hipLaunchKernelGGL((rq_seg_kernel<Q, B, RANK_NONE, 0>), grid, dim3(256), 0, s, a); break;
     case RANK_LOCAL: hipLaunchKernelGGL((rq_seg_kernel<Q, B, RANK_LOCAL, 8>), grid, dim3(256), 0, s, a); break;
-    default: hipLaunchKernelGGL((rq_seg_kernel<Q, B, RANK_PARTIAL, 64>), grid, dim3(256), 0, s, a); break;
+    default:
+        if (a.k <= 16) hipLaunchKernelGGL((rq_seg_kernel<Q, B, RANK_PARTIAL, 16>), grid, dim3(256), 0, s, a);
+        else hipLaunchKernelGGL((rq_seg_kernel<Q, B, RANK_PARTIAL, 64>), grid, dim3(256), 0, s, a);
+        break;
     }
     return check_launch("rq_seg_kernel");
 }
@@ -292,6 +295,42 @@ int launch_prepare(const float *v, const float *wt, int64_t n, int k, void *prep
     return NARHIP_OK;
 }
 
+// Splits of the fp64 VALU projection (16-token tiles): about 1024 workgroups,
+// each split a whole number of 128-channel blocks.
+int f64_splits(int64_t T, int64_t n)
+{
+    const int64_t tiles = (T + 15) / 16;
+    int s = 1;
+    while (s < 64 && tiles * s * 2 <= 1024 && n % (128 * 2 * (int64_t)s) == 0) s *= 2;
+    return s;
+}
+int f64_kmax(int k) { return k <= 8 ? 8 : 16; }
+
+int launch_proj_f64(const uint16_t *x, int64_t T, int64_t n, int64_t ldx, const float *v, int k, int splits,
+                    double *pd, hipStream_t s)
+{
+    if (T == 0) return NARHIP_OK;
+    ProjF64Args a{x, ldx, T, n, v, pd, k, splits};
+    dim3 grid((unsigned)((T + 15) / 16), (unsigned)splits);
+    if (k <= 8) hipLaunchKernelGGL((proj_f64_kernel<8>), grid, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((proj_f64_kernel<16>), grid, dim3(256), 0, s, a);
+    return check_launch("proj_f64_kernel");
+}
+
+int launch_fold_f64(const double *pd, int splits, int kmax, int k, int64_t T, float *u, hipStream_t s)
+{
+    const int64_t n = T * k;
+    hipLaunchKernelGGL(fold_f64_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, pd, splits, kmax, k, T, u);
+    return check_launch("fold_f64_kernel");
+}
+
+int launch_fold_f32(const float *partial, int splits, int k, int64_t T, float *u, hipStream_t s)
+{
+    const int64_t n = T * k;
+    hipLaunchKernelGGL(fold_f32_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, partial, splits, k, T, u);
+    return check_launch("fold_f32_kernel");
+}
+
 // Channel splits for the MFMA projection: enough workgroups for two per CU
 // (128-token tiles, splits of a multiple of 128 channels).
 int mfma_splits(int64_t T, int64_t n)
@@ -438,7 +477,7 @@ struct Plan {
     Path path;
     bool kron;
     int seg_mode;
-    bool need_prep, need_proj, need_P, need_corr;
+    bool need_prep, need_proj, need_P, need_corr, vproj;
     int splits;
     int64_t chunk;
     size_t prep_b, proj_b, P_b, corr_b, u_b;
@@ -495,8 +534,15 @@ int make_plan(int64_t T, int64_t n, int m, int q, int k, int64_t nb, bool have_p
         return NARHIP_OK;
     }
     p.need_proj = !have_partial;
-    p.splits = have_partial ? splits : 1;
-    p.proj_b = p.need_proj ? sizeof(float) * (size_t)T * (size_t)k : 0;
+    // exact mode: the fp64 projection in one split, u one fp64 sum rounded once
+    // (bit-exact); otherwise the fp64 VALU projection over channel splits with
+    // fp64 partials, folded once
+    p.vproj = p.need_proj && !exact && k <= 16;
+    p.splits = have_partial ? splits : (p.vproj ? f64_splits(T, n) : 1);
+    p.proj_b = !p.need_proj ? 0
+               : p.vproj ? sizeof(double) * (size_t)T * (size_t)p.splits * (size_t)f64_kmax(k)
+                         : sizeof(float) * (size_t)T * (size_t)k;
+    if (p.vproj || p.splits > 1) p.u_b = sizeof(float) * (size_t)T * (size_t)k;   // folded u
     if (p.kron) {
         p.path = PATH_KRON_EXACT;
         p.need_corr = true;
@@ -520,8 +566,9 @@ int run_rotate_quant(const void *x_bf16, int64_t T, int64_t n, int64_t ldx, int 
     if (q % group) return fail(NARHIP_EINVAL, "group %d must divide the Hadamard block %d", group, q);
     if (ldx < n || ldx % 8) return fail(NARHIP_EINVAL, "ld_x=%lld must be >= n and a multiple of 8", (long long)ldx);
     if (T > 0 && (!x_bf16 || !codes || !scales || !zeros)) return fail(NARHIP_EINVAL, "null tensor argument");
-    if (!aligned16(x_bf16) || !aligned16(codes) || (rotated && !aligned16(rotated)) || !aligned16(prepared))
-        return fail(NARHIP_EINVAL, "x, codes, rotated and prepared must be 16-byte aligned");
+    if (!aligned16(x_bf16) || !aligned16(codes) || (rotated && !aligned16(rotated)) || !aligned16(prepared) ||
+        !aligned16(wt))
+        return fail(NARHIP_EINVAL, "x, codes, rotated, prepared and w_t must be 16-byte aligned");
     if (k > 0 && p.path != PATH_SEG && !prepared && !wt) return fail(NARHIP_EINVAL, "rank factor w_t missing");
     if (k > 0 && (p.need_proj || p.seg_mode == RANK_LOCAL) && !v && !(p.path == PATH_MFMA_RANK && prepared))
         return fail(NARHIP_EINVAL, "rank factor v missing");
@@ -597,9 +644,20 @@ int run_rotate_quant(const void *x_bf16, int64_t T, int64_t n, int64_t ldx, int 
 
     const float *part = partial;
     int sp = splits;
-    if (p.need_proj) {
+    float *uf = reinterpret_cast<float *>(u3);
+    if (p.vproj) {
+        double *pd = reinterpret_cast<double *>(proj);
+        if ((rc = launch_proj_f64(x, T, n, ldx, v, k, p.splits, pd, s))) return rc;
+        if ((rc = launch_fold_f64(pd, p.splits, f64_kmax(k), k, T, uf, s))) return rc;
+        part = uf;
+        sp = 1;
+    } else if (p.need_proj) {
         if ((rc = launch_proj_exact(x, T, n, ldx, v, k, 1, proj, s))) return rc;
         part = proj;
+        sp = 1;
+    } else if (sp > 1 && uf) {
+        if ((rc = launch_fold_f32(part, sp, k, T, uf, s))) return rc;
+        part = uf;
         sp = 1;
     }
     if (p.kron) {

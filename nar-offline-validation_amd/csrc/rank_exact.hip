@@ -75,6 +75,124 @@ proj_exact_kernel(ProjArgs a)
     }
 }
 
+// Projection on fp64 VALU for small ranks (k <= KMAX <= 16): fp64 partial sums
+// per channel split, pd[t][s][KMAX] (internal workspace layout), folded by
+// fold_f64_kernel into u = RN32(total).  Exact products, fp64 sums (the order
+// of the fp64 additions differs from a sequential sum only by fp64 rounding).
+//
+// grid (ceil(T/16), splits), block 256: wave w owns tokens 4w..4w+3 of the
+// 16-token tile, lane l the channel pairs c_begin + 2l + 128j of the split.  A
+// lane keeps V of its two channels in fp64 registers and the 4 x KMAX running
+// sums; x arrives as one 4-byte load per token (256 bytes per wave).  The lane
+// sums are combined across the wave once per split (DPP within rows, then
+// across rows).
+struct ProjF64Args {
+    const uint16_t *x;
+    int64_t ldx, T, n;
+    const float *v;         // [n, k]
+    double *pd;             // [T][splits][KMAX]
+    int k, splits;
+};
+
+__device__ __forceinline__ double wave_sum64(double v)
+{
+    v += xchg64<0>(v);
+    v += xchg64<1>(v);
+    v += xchg64<2>(v);
+    v += xchg64<3>(v);
+    v += __shfl_xor(v, 16);
+    v += __shfl_xor(v, 32);
+    return v;
+}
+
+template <int KMAX>
+__global__ void __launch_bounds__(256)
+proj_f64_kernel(ProjF64Args a)
+{
+    constexpr int TT = 4;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, w = tid >> 6;
+    const int64_t t0 = (int64_t)blockIdx.x * 16 + TT * w;
+    const int split = blockIdx.y;
+    const int64_t chunk = a.n / a.splits;
+    const int64_t c_begin = split * chunk, c_end = c_begin + chunk;
+    const uint16_t *xr[TT];
+#pragma unroll
+    for (int tt = 0; tt < TT; tt++) {
+        const int64_t t = t0 + tt < a.T ? t0 + tt : a.T - 1;
+        xr[tt] = a.x + t * a.ldx;
+    }
+    double acc[TT][KMAX];
+#pragma unroll
+    for (int tt = 0; tt < TT; tt++)
+#pragma unroll
+        for (int r = 0; r < KMAX; r++) acc[tt][r] = 0.0;
+    for (int64_t c = c_begin + 2 * lane; c < c_end; c += 128) {
+        double v0[KMAX], v1[KMAX];
+        if (a.k == KMAX) {
+            // rows c and c+1 of V: 2 KMAX contiguous floats, 32-byte aligned
+            const float4 *vr = reinterpret_cast<const float4 *>(a.v + c * KMAX);
+#pragma unroll
+            for (int q = 0; q < KMAX / 4; q++) {
+                const float4 f0 = vr[q], f1 = vr[KMAX / 4 + q];
+                v0[4 * q] = f0.x; v0[4 * q + 1] = f0.y; v0[4 * q + 2] = f0.z; v0[4 * q + 3] = f0.w;
+                v1[4 * q] = f1.x; v1[4 * q + 1] = f1.y; v1[4 * q + 2] = f1.z; v1[4 * q + 3] = f1.w;
+            }
+        } else {
+#pragma unroll
+            for (int r = 0; r < KMAX; r++) {
+                v0[r] = r < a.k ? (double)a.v[c * a.k + r] : 0.0;
+                v1[r] = r < a.k ? (double)a.v[(c + 1) * a.k + r] : 0.0;
+            }
+        }
+#pragma unroll
+        for (int tt = 0; tt < TT; tt++) {
+            const uint32_t xw = *reinterpret_cast<const uint32_t *>(xr[tt] + c);
+            const double x0 = (double)bf16lo(xw), x1 = (double)bf16hi(xw);
+#pragma unroll
+            for (int r = 0; r < KMAX; r++) acc[tt][r] = fma(x1, v1[r], fma(x0, v0[r], acc[tt][r]));
+        }
+    }
+#pragma unroll
+    for (int tt = 0; tt < TT; tt++) {
+        const int64_t t = t0 + tt;
+#pragma unroll
+        for (int r = 0; r < KMAX; r++) {
+            const double sum = wave_sum64(acc[tt][r]);
+            if (lane == 0 && t < a.T) a.pd[(t * a.splits + split) * KMAX + r] = sum;
+        }
+    }
+}
+
+// u[t, r] = RN32( sum_s pd[t][s][r] ), fp64 partials folded in split order.
+__global__ void __launch_bounds__(256)
+fold_f64_kernel(const double *pd, int splits, int kmax, int k, int64_t T, float *u)
+{
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= T * k) return;
+    const int64_t t = idx / k;
+    const int r = (int)(idx % k);
+    const double *p = pd + t * (int64_t)splits * kmax + r;
+    double s = 0.0;
+    for (int sp = 0; sp < splits; sp++) s += p[(int64_t)sp * kmax];
+    u[idx] = (float)s;
+}
+
+// u[t, r] = RN32( sum_s partial[t, s*k + r] ), the split partials folded in
+// fp64 in split order (one thread per (t, r)).
+__global__ void __launch_bounds__(256)
+fold_f32_kernel(const float *partial, int splits, int k, int64_t T, float *u)
+{
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= T * k) return;
+    const int64_t t = idx / k;
+    const int r = (int)(idx % k);
+    const float *p = partial + t * (int64_t)splits * k + r;
+    double s = 0.0;
+    for (int sp = 0; sp < splits; sp++) s += (double)p[(int64_t)sp * k];
+    u[idx] = (float)s;
+}
+
 struct CorrArgs {
     const float *partial;   // [T, splits*k]
     int splits, k;

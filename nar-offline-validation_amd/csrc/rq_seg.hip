@@ -148,17 +148,28 @@ rq_seg_kernel(SegArgs a)
 
     // ---- rank-k correction: x' = Hx - RN32(sum_r u_r W[r, i])
     if constexpr (MODE != RANK_NONE) {
+        // per channel: fp64 sum over r in order, rounded once; W rows read as float4
 #pragma unroll
-        for (int h = 0; h < NH; h++)
+        for (int h = 0; h < NH; h++) {
+            double acc[8];
 #pragma unroll
-            for (int e = 0; e < 8; e++) {
-                const int64_t ch = base + h * 128 + chunk * 8 + e;
-                double acc = 0.0;
+            for (int e = 0; e < 8; e++) acc[e] = 0.0;
 #pragma unroll
-                for (int r = 0; r < KMAX; r++)
-                    if (r < a.k) acc = fma((double)u[r], (double)a.wt[(int64_t)r * a.n + ch], acc);
-                v[h * 8 + e] = v[h * 8 + e] - (float)acc;
+            for (int r = 0; r < KMAX; r++) {
+                if (r < a.k) {
+                    const float4 *wr =
+                        reinterpret_cast<const float4 *>(a.wt + (int64_t)r * a.n + base + h * 128 + chunk * 8);
+                    const float4 w0 = wr[0], w1 = wr[1];
+                    const double ur = (double)u[r];
+                    acc[0] = fma(ur, (double)w0.x, acc[0]); acc[1] = fma(ur, (double)w0.y, acc[1]);
+                    acc[2] = fma(ur, (double)w0.z, acc[2]); acc[3] = fma(ur, (double)w0.w, acc[3]);
+                    acc[4] = fma(ur, (double)w1.x, acc[4]); acc[5] = fma(ur, (double)w1.y, acc[5]);
+                    acc[6] = fma(ur, (double)w1.z, acc[6]); acc[7] = fma(ur, (double)w1.w, acc[7]);
+                }
             }
+#pragma unroll
+            for (int e = 0; e < 8; e++) v[h * 8 + e] = v[h * 8 + e] - (float)acc[e];
+        }
     }
 
     if (a.rotated && active) {

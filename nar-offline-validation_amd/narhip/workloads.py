@@ -15,6 +15,8 @@ Shapes (tokens x channels, Hadamard, rank, group):
   vcache_decode 64 x (8 heads x 128), H_128 per head, k=4 per head, b=32,
                 codes scattered into a 64 x 4096-slot packed cache
   downproj_70b  16384 x 28672, H_28 (x) H_1024, k=64, b=128
+plus the reference's E17 fused-kernel settings (block H_128, T=2048, k=8/32)
+for comparison with its published timings.
 The base seed is the reference's DEFAULT_SEED (nar/experiment.py:38).
 """
 
@@ -165,10 +167,40 @@ def downproj_70b(tokens: int = 16384) -> Workload:
     return Workload("downproj_70b", bf16_bits(x), (28, 1024), 128, v=v, w_t=w_t)
 
 
+def _e17(config: int, tokens: int, n: int, k: int, outliers: int) -> np.ndarray:
+    x = _silu_up(config, tokens, n, outliers)
+    frng = _rng(config, 3)
+    v = orthonormal(frng, n, k)
+    w_t = np.ascontiguousarray(-orthonormal(frng, n, k).T)
+    return x, v, w_t
+
+
+def e17_8b(tokens: int = 2048, k: int = 8) -> Workload:
+    """The reference's E17 fused-kernel setting (nar/e17_v3.py): Llama-3.1-8B down_proj
+    input, 2048 tokens x 14336, block H_128, full-row rank k, b=128.  SiLU(gate)*up
+    activations with 16 outlier channels x50 and orthonormal synthetic factors."""
+    x, v, w_t = _e17(6 + (k == 32), tokens, 14336, k, 16)
+    return Workload(f"e17_8b_k{k}", bf16_bits(x), (1, 128), 128, v=v, w_t=w_t)
+
+
+def e17_3b(tokens: int = 2048, k: int = 8) -> Workload:
+    """E17 on the Llama-3.2-3B down_proj width: 2048 tokens x 8192, block H_128, rank k, b=128."""
+    x, v, w_t = _e17(8 + (k == 32), tokens, 8192, k, 16)
+    return Workload(f"e17_3b_k{k}", bf16_bits(x), (1, 128), 128, v=v, w_t=w_t)
+
+
 CONFIGS = {
     "kcache_3b": kcache_3b,
     "qproj_3b": qproj_3b,
     "downproj_8b": downproj_8b,
     "vcache_decode_8b": vcache_decode_8b,
     "downproj_70b": downproj_70b,
+}
+
+# The reference's published fused-kernel settings (block H_128), for comparison only.
+REFERENCE_SETTINGS = {
+    "e17_8b_k8": lambda: e17_8b(k=8),
+    "e17_8b_k32": lambda: e17_8b(k=32),
+    "e17_3b_k8": lambda: e17_3b(k=8),
+    "e17_3b_k32": lambda: e17_3b(k=32),
 }
