@@ -135,6 +135,23 @@ int narhip_group_quant(const void *x_bf16, int64_t tokens, int64_t n, int64_t ld
 int narhip_dequantize(const uint8_t *codes, const void *scales_f16, const void *zeros_f16,
                       int64_t rows, int64_t n, int32_t group, float *out, void *stream);
 
+/* The hooks' quantizer on the GPU: dynamic_asym_int4 over rows x n elements of
+ * x (dtype 0 fp32, 1 bf16, 2 fp16), groups of `group` consecutive elements
+ * (a power of two in [8, 512] dividing n).  Outputs in the reference's tuple
+ * layout: codes uint8 [rows, n] (one code per byte), scales and zeros fp16
+ * [rows, n/group], deq [rows, n] in the input dtype.  Replaces
+ * dynamic_asym_int4 (nar/experiment.py:158-184) for device tensors. */
+int narhip_dynamic_asym_int4(const void *x, int32_t dtype, int64_t rows, int64_t n, int32_t group,
+                             uint8_t *codes, void *scales_f16, void *zeros_f16, void *deq, void *stream);
+
+/* The Kronecker Hadamard of each row alone, fp32 out [rows, n]:
+ * (H_m (x) H_q) diag(signs) x with m in {1, 12, 28} (m = 1: every aligned block
+ * of q channels), q in {128, ..., 1024}; signs fp32 [n] or NULL.  Replaces
+ * full_hadamard_rows (nar/activation_experiments.py:188-217) for the widths
+ * 12 * 2^j and 28 * 2^j and block Hadamards. */
+int narhip_hadamard_rows(const void *x_bf16, int64_t rows, int64_t n, int64_t ld_x, int32_t had_m, int32_t had_q,
+                         const float *signs, float *out, void *stream);
+
 /* Device self-test of the MFMA operand mapping the kernels rely on (no
  * counterpart in the reference): one v_mfma_f32_16x16x32_bf16 with
  * a_bf16[64*8], b_bf16[64*8] per lane, d[64*4] per lane (device memory). */

@@ -9,6 +9,7 @@
 #include "rq_row.hip"
 #include "rq_seg.hip"
 #include "dequant.hip"
+#include "hooks.hip"
 
 #include <cmath>
 #include <cstdarg>
@@ -796,6 +797,61 @@ int narhip_dequantize(const uint8_t *codes, const void *scales_f16, const void *
                        static_cast<hipStream_t>(stream), codes, static_cast<const uint16_t *>(scales_f16),
                        static_cast<const uint16_t *>(zeros_f16), rows, n, group, out);
     return check_launch("dequant_kernel");
+}
+
+int narhip_dynamic_asym_int4(const void *x, int32_t dtype, int64_t rows, int64_t n, int32_t group,
+                             uint8_t *codes, void *scales_f16, void *zeros_f16, void *deq, void *stream)
+{
+    g_error.clear();
+    if (rows < 0 || n <= 0) return fail(NARHIP_EINVAL, "bad shape rows=%lld n=%lld", (long long)rows, (long long)n);
+    if (group <= 0 || n % group)
+        return fail(NARHIP_EINVAL, "last dimension %lld is not divisible by group size %d", (long long)n, group);
+    if (group % 8 || group > 512 || (group & (group - 1)))
+        return fail(NARHIP_EUNSUPPORTED, "group size %d: need a power of two in [8, 512]", group);
+    if (dtype < DT_F32 || dtype > DT_F16) return fail(NARHIP_EINVAL, "dtype code %d", dtype);
+    if (rows == 0) return NARHIP_OK;
+    if (!x || !codes || !scales_f16 || !zeros_f16 || !deq) return fail(NARHIP_EINVAL, "null tensor argument");
+    if (!aligned16(x) || !aligned16(deq) || (reinterpret_cast<uintptr_t>(codes) & 7u))
+        return fail(NARHIP_EINVAL, "x and deq must be 16-byte aligned, codes 8-byte aligned");
+    const int64_t elems = rows * n;
+    dim3 grid((unsigned)((elems / 8 + 255) / 256));
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    uint16_t *sc = static_cast<uint16_t *>(scales_f16), *zc = static_cast<uint16_t *>(zeros_f16);
+    switch (dtype) {
+    case DT_F32: hipLaunchKernelGGL(quant_tuple_kernel<DT_F32>, grid, dim3(256), 0, s, x, elems, group, codes, sc, zc, deq); break;
+    case DT_BF16: hipLaunchKernelGGL(quant_tuple_kernel<DT_BF16>, grid, dim3(256), 0, s, x, elems, group, codes, sc, zc, deq); break;
+    default: hipLaunchKernelGGL(quant_tuple_kernel<DT_F16>, grid, dim3(256), 0, s, x, elems, group, codes, sc, zc, deq); break;
+    }
+    return check_launch("quant_tuple_kernel");
+}
+
+int narhip_hadamard_rows(const void *x_bf16, int64_t rows, int64_t n, int64_t ld_x, int32_t had_m, int32_t had_q,
+                         const float *signs, float *out, void *stream)
+{
+    g_error.clear();
+    if (rows < 0 || n <= 0) return fail(NARHIP_EINVAL, "bad shape rows=%lld n=%lld", (long long)rows, (long long)n);
+    if (!pow2(had_q) || had_q < 128 || had_q > 1024)
+        return fail(NARHIP_EUNSUPPORTED, "Hadamard block width %d: need a power of two in [128, 1024]", had_q);
+    if (had_m != 1 && had_m != 12 && had_m != 28) return fail(NARHIP_EUNSUPPORTED, "no Paley factor of order %d", had_m);
+    if ((int64_t)had_m * had_q != n && !(had_m == 1 && n % had_q == 0))
+        return fail(NARHIP_EUNSUPPORTED, "H_%d x H_%d does not tile a row of %lld", had_m, had_q, (long long)n);
+    if (ld_x < n || ld_x % 8) return fail(NARHIP_EINVAL, "ld_x=%lld must be >= n and a multiple of 8", (long long)ld_x);
+    if (rows == 0) return NARHIP_OK;
+    if (!x_bf16 || !out) return fail(NARHIP_EINVAL, "null tensor argument");
+    if (!aligned16(x_bf16) || !aligned16(out)) return fail(NARHIP_EINVAL, "x and out must be 16-byte aligned");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const uint16_t *x = static_cast<const uint16_t *>(x_bf16);
+    if (had_m > 1) {
+        KronArgs ka{};
+        ka.x = x; ka.ldx = ld_x; ka.T = rows; ka.n = n; ka.signs = signs; ka.P = out;
+        ka.paley = paley_table(had_m); ka.sq = f32_sqrt(had_q); ka.rsq = 1.0f / ka.sq;
+        ka.hm = 1.0f / f32_sqrt(had_m);
+        return launch_kron(nullptr, &ka, false, had_m, had_q, 128, s);
+    }
+    SegArgs sa{};
+    sa.x = x; sa.ldx = ld_x; sa.T = rows; sa.n = n; sa.signs = signs; sa.k = 0;
+    sa.codes = nullptr; sa.rotated = out; sa.sq = f32_sqrt(had_q); sa.rsq = 1.0f / sa.sq;
+    return launch_seg(sa, had_q, 128, RANK_NONE, s);
 }
 
 int narhip_mfma_probe(const void *a_bf16, const void *b_bf16, float *d, void *stream)

@@ -1,0 +1,109 @@
+"""GPU drop-ins for the hook-side functions of the path.
+
+The reference's fake-quant hooks (KVQuantAttention, nar/experiment.py:887-910;
+ActivationQuantHooks.quantize, nar/activation_experiments.py:603-606; the E14
+RuntimeHooks V path and the E17 DownHooks) rotate a tensor with
+``full_hadamard_rows`` and then call ``dynamic_asym_int4``.  These functions
+keep those names, signatures, return layouts and exceptions, and run on the
+HIP kernels of libnarhip.so:
+
+  dynamic_asym_int4(x, group_size) -> (deq, scale16, zero16, codes)
+      nar/experiment.py:158-184.  deq in x.dtype and x's shape; scale16 and
+      zero16 fp16 [..., G]; codes uint8 [..., G, group_size] (one per byte).
+  full_hadamard_rows(x, signs) -> (H_m (x) H_q) diag(signs) x, x's shape
+      nar/activation_experiments.py:188-217, for widths 28 * 2^j, 12 * 2^j and
+      2^j <= 1024.  The kernels read bf16 rows: x must be bf16, or fp32 holding
+      bf16 values (the hooks pass ``value.float()`` of a bf16 model).
+  rotate_dynamic_asym_int4(x, group_size, *, signs=None, v=None, w_t=None)
+      both in one call, with the optional full-row rank-k term x' = Hx + U(V^T x)
+      (w_t = W''^T = -U^T), returning dynamic_asym_int4's tuple of x'.
+
+Device tensors only; there is no CPU path.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from .ops import _p, _stream, hadamard_factors, rotate_quant
+
+_DTYPE_CODE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
+
+
+def _group_view_check(n: int, group_size: int) -> None:
+    if n % group_size:
+        raise ValueError(f"last dimension {n} is not divisible by group size {group_size}")
+
+
+def dynamic_asym_int4(x: torch.Tensor, group_size: int):
+    """Fake-quantize with one fp16 scale and fp16 zero per group of the last dimension."""
+    if not x.is_cuda:
+        raise ValueError("dynamic_asym_int4 (narhip) takes device tensors")
+    if x.dtype not in _DTYPE_CODE:
+        raise ValueError(f"unsupported dtype {x.dtype}")
+    n = x.shape[-1]
+    _group_view_check(n, group_size)
+    xc = x.contiguous()
+    rows = xc.numel() // n if n else 0
+    lead = tuple(x.shape[:-1])
+    groups = n // group_size
+    codes = torch.empty(lead + (groups, group_size), dtype=torch.uint8, device=x.device)
+    scales = torch.empty(lead + (groups,), dtype=torch.float16, device=x.device)
+    zeros = torch.empty(lead + (groups,), dtype=torch.float16, device=x.device)
+    deq = torch.empty_like(xc)
+    _lib.check(_lib.load().narhip_dynamic_asym_int4(_p(xc), _DTYPE_CODE[x.dtype], rows, n, group_size,
+                                                    _p(codes), _p(scales), _p(zeros), _p(deq),
+                                                    _stream(x.device)))
+    return deq.view(x.shape), scales, zeros, codes
+
+
+def _as_bf16_rows(x: torch.Tensor) -> torch.Tensor:
+    n = x.shape[-1]
+    if x.dtype == torch.bfloat16:
+        xb = x
+    elif x.dtype == torch.float32:
+        xb = x.to(torch.bfloat16)
+        if not torch.equal(xb.float(), x):
+            raise ValueError("full_hadamard_rows (narhip) reads bf16 rows: x holds values that are not bf16")
+    else:
+        raise ValueError(f"unsupported dtype {x.dtype}")
+    return xb.contiguous().view(-1, n)
+
+
+def _signs_f32(signs: torch.Tensor | None, n: int, device: torch.device) -> torch.Tensor | None:
+    if signs is None:
+        return None
+    s = signs.to(device=device, dtype=torch.float32).contiguous().view(-1)
+    if s.numel() != n:
+        raise ValueError(f"signs must have {n} entries")
+    return s
+
+
+def full_hadamard_rows(x: torch.Tensor, signs: torch.Tensor | None) -> torch.Tensor:
+    """(H_m (x) H_q) diag(signs) x along the last dimension, fp32 out, x's shape."""
+    if not x.is_cuda:
+        raise ValueError("full_hadamard_rows (narhip) takes device tensors")
+    n = x.shape[-1]
+    m, q = hadamard_factors(n)
+    xb = _as_bf16_rows(x)
+    out = torch.empty(xb.shape, dtype=torch.float32, device=x.device)
+    s = _signs_f32(signs, n, x.device)
+    _lib.check(_lib.load().narhip_hadamard_rows(_p(xb), xb.shape[0], n, n, m, q, _p(s), _p(out),
+                                                _stream(x.device)))
+    return out.view(x.shape)
+
+
+def rotate_dynamic_asym_int4(x: torch.Tensor, group_size: int, *, signs: torch.Tensor | None = None,
+                             v: torch.Tensor | None = None, w_t: torch.Tensor | None = None):
+    """dynamic_asym_int4 of x' = (H_m (x) H_q) diag(signs) x + U (V^T x); tuple of x' in fp32."""
+    if not x.is_cuda:
+        raise ValueError("rotate_dynamic_asym_int4 (narhip) takes device tensors")
+    n = x.shape[-1]
+    _group_view_check(n, group_size)
+    m, q = hadamard_factors(n)
+    xb = _as_bf16_rows(x)
+    rot = torch.empty(xb.shape, dtype=torch.float32, device=x.device)
+    rotate_quant(xb, hadamard=(m, q), signs=_signs_f32(signs, n, x.device), v=v, w_t=w_t,
+                 group=128, rotated=rot)
+    return dynamic_asym_int4(rot.view(x.shape), group_size)
