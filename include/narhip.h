@@ -152,6 +152,30 @@ int narhip_dynamic_asym_int4(const void *x, int32_t dtype, int64_t rows, int64_t
 int narhip_hadamard_rows(const void *x_bf16, int64_t rows, int64_t n, int64_t ld_x, int32_t had_m, int32_t had_q,
                          const float *signs, float *out, void *stream);
 
+/* E28's down_proj transform, fp16 in and fp16 out, no quantization:
+ * out = fp16( H_q-blocks(x) / fp32(sqrt q) - RN32(u W^T) ) per row of x fp16
+ * [tokens, ld_x], q in {128, ..., 1024} (E28: 128), w_t fp32 [k, n], k <= 16.
+ * u comes from `partial` fp32 [tokens, splits*k] (the split partials of
+ * narhip_rank_projection_f16, folded in split order; Kernel B alone) or, with
+ * partial NULL, is computed here from v fp32 [n, k] (u = RN32(x V), fp64
+ * sums) in a workspace of narhip_transform_f16_workspace() bytes.  k = 0:
+ * Hadamard blocks only.  Replaces NARDownTransform.forward
+ * (quarot-llama3/nar_r4_kernel.py:256-275) and launch_kernel_b with its
+ * kernels nar_group_transform_kernel / nar_group_transform_tc_kernel
+ * (quarot-llama3/nar_r4_kernel.py:56-120, :155-175). */
+int narhip_transform_f16(const void *x_f16, int64_t tokens, int64_t n, int64_t ld_x, int32_t had_q,
+                         const float *v, const float *partial, int32_t splits, const float *w_t, int32_t k,
+                         void *out_f16, void *workspace, size_t workspace_bytes, void *stream);
+size_t narhip_transform_f16_workspace(int64_t tokens, int64_t n, int32_t k);
+
+/* Kernel A of the E28 transform on fp16 rows: partial[t, s*k + r] =
+ * RN32(sum over channel split s of x[t, i] v[i, r]) with fp64 sums, v fp32
+ * [n, k], 1 <= k <= 16, n / splits even.  Replaces launch_projection_dot on fp16
+ * input with TERMS = 2 fp16 factor terms (quarot-llama3/nar_r4_kernel.py:272,
+ * nar/kernels/r4_fused_v3.py:187-201). */
+int narhip_rank_projection_f16(const void *x_f16, int64_t tokens, int64_t n, int64_t ld_x, const float *v,
+                               int32_t k, int32_t splits, float *partial, void *stream);
+
 /* Device self-test of the MFMA operand mapping the kernels rely on (no
  * counterpart in the reference): one v_mfma_f32_16x16x32_bf16 with
  * a_bf16[64*8], b_bf16[64*8] per lane, d[64*4] per lane (device memory). */

@@ -308,13 +308,18 @@ int f64_splits(int64_t T, int64_t n)
 int f64_kmax(int k) { return k <= 8 ? 8 : 16; }
 
 int launch_proj_f64(const uint16_t *x, int64_t T, int64_t n, int64_t ldx, const float *v, int k, int splits,
-                    double *pd, hipStream_t s)
+                    double *pd, hipStream_t s, bool f16 = false, float *pf = nullptr)
 {
     if (T == 0) return NARHIP_OK;
-    ProjF64Args a{x, ldx, T, n, v, pd, k, splits};
+    ProjF64Args a{x, ldx, T, n, v, pd, k, splits, pf};
     dim3 grid((unsigned)((T + 15) / 16), (unsigned)splits);
-    if (k <= 8) hipLaunchKernelGGL((proj_f64_kernel<8>), grid, dim3(256), 0, s, a);
-    else hipLaunchKernelGGL((proj_f64_kernel<16>), grid, dim3(256), 0, s, a);
+    if (f16) {
+        if (k <= 8) hipLaunchKernelGGL((proj_f64_kernel<8, true>), grid, dim3(256), 0, s, a);
+        else hipLaunchKernelGGL((proj_f64_kernel<16, true>), grid, dim3(256), 0, s, a);
+    } else {
+        if (k <= 8) hipLaunchKernelGGL((proj_f64_kernel<8>), grid, dim3(256), 0, s, a);
+        else hipLaunchKernelGGL((proj_f64_kernel<16>), grid, dim3(256), 0, s, a);
+    }
     return check_launch("proj_f64_kernel");
 }
 
@@ -852,6 +857,84 @@ int narhip_hadamard_rows(const void *x_bf16, int64_t rows, int64_t n, int64_t ld
     sa.x = x; sa.ldx = ld_x; sa.T = rows; sa.n = n; sa.signs = signs; sa.k = 0;
     sa.codes = nullptr; sa.rotated = out; sa.sq = f32_sqrt(had_q); sa.rsq = 1.0f / sa.sq;
     return launch_seg(sa, had_q, 128, RANK_NONE, s);
+}
+
+size_t narhip_transform_f16_workspace(int64_t tokens, int64_t n, int32_t k)
+{
+    if (tokens <= 0 || n <= 0 || k <= 0 || k > 16) return 0;
+    const int sp = f64_splits(tokens, n);
+    return align256(sizeof(double) * (size_t)tokens * (size_t)sp * (size_t)f64_kmax(k)) +
+           align256(sizeof(float) * (size_t)tokens * (size_t)k);
+}
+
+int narhip_rank_projection_f16(const void *x_f16, int64_t tokens, int64_t n, int64_t ld_x, const float *v,
+                               int32_t k, int32_t splits, float *partial, void *stream)
+{
+    g_error.clear();
+    if (tokens < 0 || n <= 0 || ld_x < n || ld_x % 8) return fail(NARHIP_EINVAL, "bad shape");
+    if (k < 1 || k > 16) return fail(NARHIP_EUNSUPPORTED, "fp16 projection supports rank k in [1, 16] (got %d)", k);
+    if (splits < 1 || n % splits || (n / splits) % 2)
+        return fail(NARHIP_EINVAL, "%lld channels do not divide into %d even splits", (long long)n, splits);
+    if (tokens == 0) return NARHIP_OK;
+    if (!x_f16 || !v || !partial) return fail(NARHIP_EINVAL, "null tensor argument");
+    if (!aligned16(x_f16) || !aligned16(v)) return fail(NARHIP_EINVAL, "x and v must be 16-byte aligned");
+    return launch_proj_f64(static_cast<const uint16_t *>(x_f16), tokens, n, ld_x, v, k, splits, nullptr,
+                           static_cast<hipStream_t>(stream), true, partial);
+}
+
+int narhip_transform_f16(const void *x_f16, int64_t tokens, int64_t n, int64_t ld_x, int32_t had_q,
+                         const float *v, const float *partial, int32_t splits, const float *w_t, int32_t k,
+                         void *out_f16, void *workspace, size_t workspace_bytes, void *stream)
+{
+    g_error.clear();
+    if (tokens < 0 || n <= 0) return fail(NARHIP_EINVAL, "bad shape tokens=%lld n=%lld", (long long)tokens, (long long)n);
+    if (!pow2(had_q) || had_q < 128 || had_q > 1024 || n % had_q)
+        return fail(NARHIP_EUNSUPPORTED, "block Hadamard width %d must be a power of two in [128, 1024] dividing n",
+                    had_q);
+    if (k < 0 || k > 16) return fail(NARHIP_EUNSUPPORTED, "fp16 transform supports rank k <= 16 (got %d)", k);
+    if (ld_x < n || ld_x % 8) return fail(NARHIP_EINVAL, "ld_x=%lld must be >= n and a multiple of 8", (long long)ld_x);
+    if (partial && (splits < 1 || k < 1)) return fail(NARHIP_EINVAL, "partials need splits >= 1 and k >= 1");
+    const size_t need = partial ? 0 : narhip_transform_f16_workspace(tokens, n, k);
+    if (need > 0 && (!workspace || workspace_bytes < need))
+        return fail(NARHIP_EWORKSPACE, "workspace of %zu bytes required, %zu given", need, workspace_bytes);
+    if (tokens == 0) return NARHIP_OK;
+    if (!x_f16 || !out_f16 || (k > 0 && (!w_t || (!partial && !v)))) return fail(NARHIP_EINVAL, "null tensor argument");
+    if (!aligned16(x_f16) || !aligned16(out_f16) || !aligned16(w_t) || !aligned16(v))
+        return fail(NARHIP_EINVAL, "x, out, v and w_t must be 16-byte aligned");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const uint16_t *x = static_cast<const uint16_t *>(x_f16);
+    int rc;
+    SegArgs a{};
+    a.splits = 1;
+    if (partial) {
+        a.partial = partial;
+        a.splits = splits;
+    } else if (k > 0) {
+        const int sp = f64_splits(tokens, n);
+        double *pd = static_cast<double *>(workspace);
+        float *u = reinterpret_cast<float *>(static_cast<char *>(workspace) +
+                                             align256(sizeof(double) * (size_t)tokens * (size_t)sp * (size_t)f64_kmax(k)));
+        if ((rc = launch_proj_f64(x, tokens, n, ld_x, v, k, sp, pd, s, true))) return rc;
+        if ((rc = launch_fold_f64(pd, sp, f64_kmax(k), k, tokens, u, s))) return rc;
+        a.partial = u;
+    }
+    a.x = x; a.ldx = ld_x; a.T = tokens; a.n = n; a.signs = nullptr;
+    a.wt = w_t; a.k = k;
+    a.codes = nullptr; a.rotated = static_cast<float *>(out_f16);
+    a.sq = f32_sqrt(had_q); a.rsq = 1.0f / a.sq;
+    const int64_t segs = tokens * (n / had_q);
+    dim3 grid((unsigned)((segs + 15) / 16));
+#define NARHIP_F16_SEG(QQ)                                                                                      \
+    if (k > 0) hipLaunchKernelGGL((rq_seg_kernel<QQ, 128, RANK_PARTIAL, 16, true>), grid, dim3(256), 0, s, a); \
+    else hipLaunchKernelGGL((rq_seg_kernel<QQ, 128, RANK_NONE, 0, true>), grid, dim3(256), 0, s, a);
+    switch (had_q) {
+    case 128: NARHIP_F16_SEG(128) break;
+    case 256: NARHIP_F16_SEG(256) break;
+    case 512: NARHIP_F16_SEG(512) break;
+    default: NARHIP_F16_SEG(1024) break;
+    }
+#undef NARHIP_F16_SEG
+    return check_launch("rq_seg_kernel (fp16)");
 }
 
 int narhip_mfma_probe(const void *a_bf16, const void *b_bf16, float *d, void *stream)

@@ -87,11 +87,12 @@ proj_exact_kernel(ProjArgs a)
 // sums are combined across the wave once per split (DPP within rows, then
 // across rows).
 struct ProjF64Args {
-    const uint16_t *x;
+    const uint16_t *x;      // bf16 or (F16) fp16 rows
     int64_t ldx, T, n;
     const float *v;         // [n, k]
-    double *pd;             // [T][splits][KMAX]
+    double *pd;             // [T][splits][KMAX], or null when pf is set
     int k, splits;
+    float *pf;              // null, or fp32 partials [T, splits*k] (each split rounded once)
 };
 
 __device__ __forceinline__ double wave_sum64(double v)
@@ -105,7 +106,7 @@ __device__ __forceinline__ double wave_sum64(double v)
     return v;
 }
 
-template <int KMAX>
+template <int KMAX, bool F16 = false>
 __global__ void __launch_bounds__(256)
 proj_f64_kernel(ProjF64Args a)
 {
@@ -148,7 +149,8 @@ proj_f64_kernel(ProjF64Args a)
 #pragma unroll
         for (int tt = 0; tt < TT; tt++) {
             const uint32_t xw = *reinterpret_cast<const uint32_t *>(xr[tt] + c);
-            const double x0 = (double)bf16lo(xw), x1 = (double)bf16hi(xw);
+            const double x0 = F16 ? (double)f16_bits_to_f32((uint16_t)(xw & 0xffffu)) : (double)bf16lo(xw);
+            const double x1 = F16 ? (double)f16_bits_to_f32((uint16_t)(xw >> 16)) : (double)bf16hi(xw);
 #pragma unroll
             for (int r = 0; r < KMAX; r++) acc[tt][r] = fma(x1, v1[r], fma(x0, v0[r], acc[tt][r]));
         }
@@ -159,7 +161,13 @@ proj_f64_kernel(ProjF64Args a)
 #pragma unroll
         for (int r = 0; r < KMAX; r++) {
             const double sum = wave_sum64(acc[tt][r]);
-            if (lane == 0 && t < a.T) a.pd[(t * a.splits + split) * KMAX + r] = sum;
+            if (lane == 0 && t < a.T) {
+                if (a.pf) {
+                    if (r < a.k) a.pf[(t * a.splits + split) * a.k + r] = (float)sum;
+                } else {
+                    a.pd[(t * a.splits + split) * KMAX + r] = sum;
+                }
+            }
         }
     }
 }

@@ -34,7 +34,9 @@ struct SegArgs {
     float sq, rsq;          // fp32(sqrt(Q)) and RN(1/sq), computed on the host
 };
 
-template <int Q, int B, int MODE, int KMAX>
+// F16IO: fp16 rows in, fp16 rows out (the E28 transform epilogue: no
+// quantization; `rotated` then points to fp16 [T, n]), else bf16 in and INT4 out.
+template <int Q, int B, int MODE, int KMAX, bool F16IO = false>
 __global__ void __launch_bounds__(256)
 rq_seg_kernel(SegArgs a)
 {
@@ -63,8 +65,13 @@ rq_seg_kernel(SegArgs a)
     }
 #pragma unroll
     for (int i = 0; i < NV / 2; i++) {
-        v[2 * i] = bf16lo(raw[i]);
-        v[2 * i + 1] = bf16hi(raw[i]);
+        if constexpr (F16IO) {
+            v[2 * i] = f16_bits_to_f32((uint16_t)(raw[i] & 0xffffu));
+            v[2 * i + 1] = f16_bits_to_f32((uint16_t)(raw[i] >> 16));
+        } else {
+            v[2 * i] = bf16lo(raw[i]);
+            v[2 * i + 1] = bf16hi(raw[i]);
+        }
     }
 
     // ---- rank-k projection of the raw input (fp64, rounded once to fp32)
@@ -172,6 +179,21 @@ rq_seg_kernel(SegArgs a)
         }
     }
 
+    if constexpr (F16IO) {
+        if (active) {
+            uint16_t *o = reinterpret_cast<uint16_t *>(a.rotated) + t * a.n + base;
+#pragma unroll
+            for (int h = 0; h < NH; h++) {
+                uint32_t w[4];
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    w[j] = (uint32_t)f32_to_f16_bits(v[h * 8 + 2 * j]) |
+                           ((uint32_t)f32_to_f16_bits(v[h * 8 + 2 * j + 1]) << 16);
+                *reinterpret_cast<uint4 *>(o + h * 128 + chunk * 8) = make_uint4(w[0], w[1], w[2], w[3]);
+            }
+        }
+        return;
+    }
     if (a.rotated && active) {
         float *o = a.rotated + t * a.n + base;
 #pragma unroll

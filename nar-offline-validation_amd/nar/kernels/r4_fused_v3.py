@@ -1,9 +1,10 @@
 """Drop-in for nar/kernels/r4_fused_v3.py on MI355X (HIP kernels in libnarhip.so).
 
 Same names and signatures as the reference module (nar/kernels/r4_fused_v3.py:
-39-271).  ``launch_projection_dot`` takes the reference's stacked bf16 factor
-terms (y_padded [TERMS*n, KP]), rebuilds the fp32 factor they represent and
-runs narhip's Kernel A on bf16 MFMA; ``launch_nar`` / ``launch_hadamard`` run
+39-271).  ``launch_projection_dot`` takes the reference's stacked bf16 (or, for
+fp16 rows, fp16) factor terms (y_padded [TERMS*n, KP]), rebuilds the fp32
+factor they represent and runs narhip's Kernel A (bf16 MFMA, or fp64 VALU for
+fp16 rows); ``launch_nar`` / ``launch_hadamard`` run
 narhip's Kernel B.  The Triton tile dataclasses and config lists are kept so
 that the reference's verify-then-time harnesses run unchanged: the HIP kernels
 pick their own tiles, so ``block_t``/``num_warps``/``num_stages``/``use_dot``
@@ -130,6 +131,10 @@ def launch_projection_dot(x: torch.Tensor, y_padded: torch.Tensor, partial: torc
     if partial.shape != (tokens, config.splits * k):
         raise ValueError(f"partial must be [{tokens}, {config.splits * k}]")
     v = _factor_from_terms(y_padded, n, k, terms)
+    if x.dtype == torch.float16:
+        # E28 feeds fp16 rows with TERMS = 2 fp16 factor terms
+        # (quarot-llama3/nar_r4_kernel.py:267,272): fp64 VALU projection.
+        return ops.rank_projection_f16(x, v, partial)
     if n % (128 * config.splits) == 0:
         prep = cached_prepared(v, None, n, k)
         return ops.rank_projection(x, v, partial, ops.RANK_MFMA, prepared=prep)

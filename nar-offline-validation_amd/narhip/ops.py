@@ -173,6 +173,73 @@ def rank_projection(x: torch.Tensor, v: torch.Tensor | None, partial: torch.Tens
     return partial
 
 
+def rank_projection_f16(x: torch.Tensor, v: torch.Tensor, partial: torch.Tensor) -> torch.Tensor:
+    """fp16 rows: partial[t, s*k + r] = RN32(sum over channel split s of x[t, i] v[i, r]), fp64 sums."""
+    if x.dtype != torch.float16 or x.dim() != 2 or x.stride(1) != 1:
+        raise ValueError("x must be a float16 [tokens, n] tensor with contiguous rows")
+    if not x.is_cuda:
+        raise ValueError("x must be a GPU tensor")
+    dev = x.device
+    _require(v, torch.float32, "v", dev)
+    _require(partial, torch.float32, "partial", dev)
+    T, n = x.shape
+    k = int(v.shape[1])
+    if v.shape[0] != n:
+        raise ValueError(f"v must be [{n}, k], got {tuple(v.shape)}")
+    if partial.shape[0] != T or partial.shape[1] % k:
+        raise ValueError("partial must be [tokens, splits*k]")
+    splits = partial.shape[1] // k
+    rc = _lib.load().narhip_rank_projection_f16(_p(x), T, n, x.stride(0), _p(v), k, splits, _p(partial),
+                                                _stream(dev))
+    _lib.check(rc)
+    return partial
+
+
+def transform_f16(x: torch.Tensor, w_t: torch.Tensor | None, *, v: torch.Tensor | None = None,
+                  partial: torch.Tensor | None = None, had_q: int = 128,
+                  out: torch.Tensor | None = None) -> torch.Tensor:
+    """fp16 [tokens, n] -> fp16: Hadamard blocks of had_q, minus u W^T (E28's transform).
+
+    u is folded from `partial` [tokens, splits*k] when given, else computed from
+    v [n, k]; w_t is fp32 [k, n] (None: Hadamard blocks only).
+    """
+    if x.dtype != torch.float16 or x.dim() != 2 or x.stride(1) != 1:
+        raise ValueError("x must be a float16 [tokens, n] tensor with contiguous rows")
+    if not x.is_cuda:
+        raise ValueError("x must be a GPU tensor")
+    dev = x.device
+    T, n = x.shape
+    k = 0 if w_t is None else int(w_t.shape[0])
+    splits = 0
+    if k:
+        _require(w_t, torch.float32, "w_t", dev)
+        if w_t.shape[1] != n:
+            raise ValueError(f"w_t must be [k, {n}], got {tuple(w_t.shape)}")
+        if partial is not None:
+            _require(partial, torch.float32, "partial", dev)
+            if partial.shape[0] != T or partial.shape[1] % k:
+                raise ValueError(f"partial must be [{T}, splits*{k}]")
+            splits = partial.shape[1] // k
+        else:
+            if v is None:
+                raise ValueError("the rank term needs v or partial")
+            _require(v, torch.float32, "v", dev)
+            if tuple(v.shape) != (n, k):
+                raise ValueError(f"v must be [{n}, {k}], got {tuple(v.shape)}")
+    if out is None:
+        out = torch.empty((T, n), dtype=torch.float16, device=dev)
+    else:
+        _require(out, torch.float16, "out", dev)
+    lib = _lib.load()
+    ws_bytes = 0 if partial is not None else lib.narhip_transform_f16_workspace(T, n, k)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
+    rc = lib.narhip_transform_f16(_p(x), T, n, x.stride(0), had_q, _p(v) if k else None,
+                                  _p(partial) if k else None, splits, _p(w_t), k, _p(out), _p(ws), ws_bytes,
+                                  _stream(dev))
+    _lib.check(rc)
+    return out
+
+
 def group_quant(x: torch.Tensor, partial: torch.Tensor | None, w_t: torch.Tensor | None,
                 codes: torch.Tensor, scales: torch.Tensor, zeros: torch.Tensor, *,
                 hadamard: tuple[int, int] = (1, 128), group: int = 128,

@@ -89,6 +89,51 @@ def test_hadamard_factor_dispatch_order():
     assert hadamard_factors(28672) == (28, 1024)
     assert hadamard_factors(3072) == (12, 256)
     assert hadamard_factors(4096) == (1, 4096)
-    assert hadamard_factors(336) == (28, 12) if False else True
     with pytest.raises(ValueError):
         hadamard_factors(1000)
+
+
+def _tf(lib, **kw):
+    a = dict(x=None, T=4, n=8192, ld=8192, q=128, v=None, partial=None, splits=0, wt=None, k=0, out=None,
+             ws=None, wsb=0, stream=None)
+    a.update(kw)
+    return lib.narhip_transform_f16(*a.values())
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(q=96), -2),                               # not a power of two
+    (dict(q=2048), -2),
+    (dict(n=8064, ld=8064, q=256), -2),             # 256 does not divide n
+    (dict(k=17, wt=16, v=16), -2),                  # rank beyond the fp16 path
+    (dict(ld=8190), -1),
+    (dict(k=8, wt=16, partial=16, splits=0), -1),   # partials without splits
+    (dict(k=8, wt=16, v=16, x=16, out=16), -4),     # projection workspace missing
+    (dict(k=8, x=16, out=16, partial=16, splits=2), -1),   # W^T missing
+])
+def test_transform_f16_host_validation(kw, code):
+    import narhip
+    lib = narhip.load()
+    assert _tf(lib, **kw) == code
+    assert lib.narhip_last_error_string() != b""
+
+
+def test_transform_f16_workspace_query():
+    import narhip
+    lib = narhip.load()
+    assert lib.narhip_transform_f16_workspace(2048, 14336, 0) == 0
+    assert lib.narhip_transform_f16_workspace(2048, 14336, 17) == 0
+    ws = lib.narhip_transform_f16_workspace(2048, 14336, 8)
+    assert ws >= 2048 * 8 * 4 + 2048 * 8 * 8 and ws % 256 == 0
+
+
+@pytest.mark.parametrize("k,n,splits,code", [
+    (0, 14336, 1, -2), (17, 14336, 1, -2),
+    (8, 14336, 3, -1),          # 3 does not divide n
+    (8, 14343, 7, -1),          # 7 x 2049: odd channel chunks
+])
+def test_rank_projection_f16_host_validation(k, n, splits, code):
+    import narhip
+    lib = narhip.load()
+    ld = (n + 7) // 8 * 8
+    assert lib.narhip_rank_projection_f16(None, 4, n, ld, None, k, splits, None, None) == code
+    assert lib.narhip_last_error_string() != b""

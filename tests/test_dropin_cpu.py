@@ -80,3 +80,27 @@ def test_e28_helpers():
     assert O.rotated_error(got, ref) < 1e-6
     row = nk.precision_row(torch.from_numpy(ref).half(), torch.from_numpy(ref))
     assert row["code_match_fraction"] > 0.99 and row["relative_l2"] < 1e-3
+
+
+def test_e28_module_host_logic():
+    import nar_r4_kernel as nk
+    rng = np.random.default_rng(3)
+    n, k = 1024, 8
+    y = torch.from_numpy(rng.standard_normal((n, k)).astype(np.float32) / 32)
+    w = torch.from_numpy(rng.standard_normal((k, n)).astype(np.float32) / 32)
+    sel = {"1": {"proj": nk.PROJECTION_CONFIGS[0].__dict__, "tile": nk.REFERENCE_TILE.__dict__},
+           "2048": {"proj": nk.PROJECTION_CONFIGS[0].__dict__, "tile": nk.TILE_CONFIGS[2].__dict__}}
+    mod = nk.NARDownTransform(y, w, k, sel)
+    assert mod.factor_bytes() == 2 * n * k * 4
+    assert mod.plan(1500)[1] == nk.TILE_CONFIGS[2] and mod.plan(2)[1] == nk.REFERENCE_TILE
+    # the reference's term buffers, built on demand for Kernel A / Kernel B harnesses
+    assert mod.y_terms.shape == (2 * n, 16) and mod.w_hi.dtype == torch.float16
+    assert mod.factor_bytes() == 2 * n * k * 4 + 2 * n * 16 * 2 + 2 * k * n * 2
+    with pytest.raises(ValueError):
+        mod(torch.zeros((2, n), dtype=torch.bfloat16))
+    with pytest.raises(ValueError):
+        mod(torch.zeros((2, n), dtype=torch.float16))          # host tensor
+    with pytest.raises(ValueError):
+        nk.NARDownTransform(torch.zeros((n, 20)), torch.zeros((20, n)), 20, sel)
+    with pytest.raises(ValueError):
+        nk.NARDownTransform(y, w[:, :512], k, sel)

@@ -1,0 +1,195 @@
+"""GPU parity of E28's fp16 down_proj transform (NARDownTransform, Kernel A + B).
+
+The oracle restates reference_transform (quarot-llama3/nar_r4_kernel.py:
+190-202) with one fp32 rounding per stage; the HIP path computes the same
+fp32 values up to the order of its fp64 projection sums, so the fp16 outputs
+are expected bit-equal, with at most 1-ulp differences on <= 1e-4 of the
+elements (a projection that lands 1 fp32 ulp apart, then an fp16 rounding
+boundary).  On top, E28's own acceptance against the fp32 reference
+(quarot-llama3/e28_bench.py:46, e28_v2/verify.py:14-16): relative L2
+<= 2e-3 and QuaRot per-token INT4 code match >= 0.999, on seeded rows and on
+the special-case inputs of e28_v2/verify.py:43-49.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+import nar_r4_kernel as nk  # noqa: E402
+from nar.kernels import r4_fused_v3 as k3  # noqa: E402
+from narhip import ops, workloads  # noqa: E402
+
+K = 8   # E28's rank (quarot-llama3/e28_bench.py RANK)
+
+
+def factors(n: int, k: int = K, seed: int = 0):
+    rng = np.random.default_rng(seed)
+    y = workloads.orthonormal(rng, n, k) * np.float32(0.75)
+    w = -workloads.orthonormal(rng, n, k).T.copy() * np.float32(1.25)
+    return np.ascontiguousarray(y, np.float32), np.ascontiguousarray(w, np.float32)
+
+
+def rows(t: int, n: int, seed: int) -> torch.Tensor:
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    x = torch.randn((t, n), generator=g) * 0.5
+    x[:, 7::997] *= 40.0                   # a few outlier channels
+    return x.half()
+
+
+def ordered(bits: np.ndarray) -> np.ndarray:
+    b = bits.astype(np.int32)
+    mag = b & 0x7FFF
+    return np.where(b & 0x8000, -mag, mag)
+
+
+def f16_ulp_report(out: torch.Tensor, ref_f32: np.ndarray) -> tuple[int, float]:
+    """(max ulp distance, fraction of elements that differ) of fp16 out vs fp16(ref)."""
+    got = out.cpu().numpy().view(np.uint16)
+    exp = ref_f32.astype(np.float16).view(np.uint16)
+    d = np.abs(ordered(got) - ordered(exp))
+    return int(d.max(initial=0)), float((d != 0).mean())
+
+
+def e28_accept(out: torch.Tensor, x: torch.Tensor, y: np.ndarray, w: np.ndarray) -> dict:
+    ref = nk.reference_transform(x.float().cpu(), torch.from_numpy(y), torch.from_numpy(w))
+    row = nk.precision_row(out.cpu(), ref)
+    assert row["relative_l2"] <= 2e-3, row
+    assert row["code_match_fraction"] >= 0.999, row
+    return row
+
+
+@pytest.mark.parametrize("tokens,n", [(1, 8192), (37, 8192), (300, 14336), (64, 3072)])
+def test_transform_matches_oracle(tokens, n):
+    print(f"[test_transform_matches_oracle] tokens={tokens} n={n}", flush=True)
+    y, w = factors(n, seed=n)
+    x = rows(tokens, n, seed=tokens)
+    mod = nk.NARDownTransform(torch.from_numpy(y), torch.from_numpy(w), K, {}).cuda()
+    out = mod(x.cuda())
+    torch.cuda.synchronize()
+    assert out.dtype == torch.float16 and out.shape == x.shape
+    ref = O.rotate(x.float().numpy(), 1, 128, v=y, wt=w)
+    worst, frac = f16_ulp_report(out, ref)
+    print(f"  max ulp {worst}, differing fraction {frac:.2e}", flush=True)
+    assert worst <= 1 and frac <= 1e-4
+    e28_accept(out, x, y, w)
+
+
+def test_transform_batched_shape():
+    print("[test_transform_batched_shape]", flush=True)
+    n = 8192
+    y, w = factors(n, seed=5)
+    x = rows(24, n, seed=5).reshape(2, 12, n)
+    mod = nk.NARDownTransform(torch.from_numpy(y), torch.from_numpy(w), K, {}).cuda()
+    out = mod(x.cuda())
+    flat = mod(x.reshape(24, n).cuda())
+    torch.cuda.synchronize()
+    assert out.shape == x.shape
+    assert torch.equal(out.reshape(24, n), flat)
+
+
+SPECIAL = ("zero", "constant", "rounding_boundary", "common_offset_small_residual", "outlier")
+
+
+def special_case(name: str, t: int, n: int) -> torch.Tensor:
+    """The special inputs of quarot-llama3/e28_v2/verify.py:43-49."""
+    g = torch.Generator(device="cpu").manual_seed(17)
+    base = torch.randn((1, n), generator=g).half()
+    if name == "zero":
+        x = torch.zeros((1, n), dtype=torch.float16)
+    elif name == "constant":
+        x = torch.full((1, n), 0.5, dtype=torch.float16)
+    elif name == "rounding_boundary":
+        x = ((torch.arange(n).float() % 15 - 7 + 0.5) / 7).half()[None, :]
+    elif name == "common_offset_small_residual":
+        x = 64 + base * 0.03125
+    else:
+        x = base.clone()
+        x[:, 0] = 128
+    return x.expand(t, -1).contiguous()
+
+
+@pytest.mark.parametrize("name", SPECIAL)
+def test_special_inputs(name):
+    print(f"[test_special_inputs] {name}", flush=True)
+    n = 8192
+    y, w = factors(n, seed=1)
+    x = special_case(name, 33, n)
+    mod = nk.NARDownTransform(torch.from_numpy(y), torch.from_numpy(w), K, {}).cuda()
+    out = mod(x.cuda())
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(out).all())
+    ref = O.rotate(x.float().numpy(), 1, 128, v=y, wt=w)
+    worst, frac = f16_ulp_report(out, ref)
+    assert worst <= 1 and frac <= 1e-4, (worst, frac)
+    e28_accept(out, x, y, w)
+    if name == "zero":
+        assert not out.float().abs().max().item()
+
+
+@pytest.mark.parametrize("splits", [1, 2, 4])
+def test_kernel_a_then_b_with_fp16_terms(splits):
+    """The E28-v2 kernel bench sequence (quarot-llama3/e28_v2/kernel_bench.py:34-35):
+    launch_projection_dot on the fp16 terms, then launch_kernel_b on w_hi / w_lo."""
+    print(f"[test_kernel_a_then_b_with_fp16_terms] splits={splits}", flush=True)
+    n, t = 14336, 96
+    y, w = factors(n, seed=2)
+    x = rows(t, n, seed=2).cuda()
+    mod = nk.NARDownTransform(torch.from_numpy(y), torch.from_numpy(w), K, {}).cuda()
+    proj = k3.ProjectionConfig(32, 128, splits, 8, 3)
+    partial = torch.empty((t, splits * K), dtype=torch.float32, device="cuda")
+    k3.launch_projection_dot(x, mod.y_terms, partial, K, proj, nk.TERMS)
+    out = torch.empty_like(x)
+    nk.launch_kernel_b(x, partial, None, out, K, nk.REFERENCE_TILE, mod.h128, mod.w_hi, mod.w_lo)
+    torch.cuda.synchronize()
+    # the factors those terms carry
+    y_t = (mod.y_terms.reshape(2, n, -1)[:, :, :K].float().sum(0)).cpu().numpy()
+    w_t = (mod.w_hi.float() + mod.w_lo.float()).cpu().numpy()
+    xs = x.float().cpu().numpy()
+    # Kernel A's per-split partials: each split rounded once to fp32 (fp64 sums)
+    chunk = n // splits
+    part = np.stack([(xs[:, s * chunk:(s + 1) * chunk].astype(np.float64)
+                      @ y_t[s * chunk:(s + 1) * chunk].astype(np.float64)).astype(np.float32)
+                     for s in range(splits)], axis=1)
+    got_p = partial.cpu().numpy().reshape(t, splits, K)
+    np.testing.assert_allclose(got_p, part, rtol=2e-6, atol=1e-6 * np.abs(part).max())
+    ref = O.rotate(xs, 1, 128, v=y_t, wt=w_t)
+    worst, frac = f16_ulp_report(out, ref)
+    print(f"  max ulp {worst}, differing fraction {frac:.2e}", flush=True)
+    assert worst <= 1 and frac <= 1e-3
+    e28_accept(out, x.cpu(), y, w)
+
+
+def test_hadamard_blocks_only_bit_exact():
+    print("[test_hadamard_blocks_only_bit_exact]", flush=True)
+    n = 8192
+    x = rows(50, n, seed=9)
+    for q in (128, 256, 512, 1024):
+        out = ops.transform_f16(x.cuda(), None, had_q=q)
+        torch.cuda.synchronize()
+        ref = O.rotate(x.float().numpy(), 1, q).astype(np.float16)
+        assert np.array_equal(out.cpu().numpy().view(np.uint16), ref.view(np.uint16)), q
+
+
+def test_select_configs_then_module():
+    print("[test_select_configs_then_module]", flush=True)
+    n = 8192
+    y, w = factors(n, seed=4)
+    yt, wt = torch.from_numpy(y).cuda(), torch.from_numpy(w).cuda()
+    tol = {"code_match_fraction_min": 0.999, "relative_l2_max": 2e-3}
+    selection, log = nk.select_configs(yt, wt, K, [1, 64], seed=0, tolerance=tol, verify_rows=64)
+    assert set(selection) == {"1", "64"} and log[0]["passes"]
+    assert all(v["pipeline_ms"] > 0 for v in selection.values())
+    mod = nk.NARDownTransform(yt, wt, K, selection)
+    assert mod.plan(50) == (k3.ProjectionConfig(**selection["64"]["proj"]), nk.TileConfig(**selection["64"]["tile"]))
+    x = rows(3, n, seed=4)
+    out = mod(x.cuda())
+    torch.cuda.synchronize()
+    worst, _ = f16_ulp_report(out, O.rotate(x.float().numpy(), 1, 128, v=y, wt=w))
+    assert worst <= 1
