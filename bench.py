@@ -53,7 +53,9 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="downproj_8b",
                     choices=["kcache_3b", "qproj_3b", "downproj_8b", "vcache_decode_8b", "downproj_70b",
-                             "e17_8b_k8", "e17_8b_k32", "e17_3b_k8", "e17_3b_k32"])
+                             "e17_8b_k8", "e17_8b_k32", "e17_3b_k8", "e17_3b_k32", "e28_8b", "e28_3b"])
+    ap.add_argument("--tokens", type=int, default=0,
+                    help="token count of the e28_* transform settings (default 2048)")
     ap.add_argument("--rank-mode", default="auto", choices=["auto", "exact", "mfma"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU baseline work")
@@ -143,8 +145,13 @@ def main() -> int:
     from narhip import ops, workloads
 
     mode = {"auto": ops.RANK_AUTO, "exact": ops.RANK_EXACT, "mfma": ops.RANK_MFMA}[args.rank_mode]
-    w = (workloads.CONFIGS.get(args.config) or workloads.REFERENCE_SETTINGS[args.config])()
+    if args.config.startswith("e28_"):
+        w = workloads.REFERENCE_SETTINGS[args.config](args.tokens or 2048)
+    else:
+        w = (workloads.CONFIGS.get(args.config) or workloads.REFERENCE_SETTINGS[args.config])()
     dev = torch.device("cuda:0")
+    if w.transform_f16:
+        return bench_transform_f16(args, w, dev)
     x_host = torch.from_numpy(w.x.view(np.int16))
     in_bytes = w.x.nbytes
     R = max(2, min(8, -(-2 * MALL_BYTES // max(in_bytes, 1)) + 1))
@@ -225,6 +232,85 @@ def main() -> int:
         line["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds)
     print(json.dumps(line), flush=True)
     return 0
+
+
+def bench_transform_f16(args, w, dev) -> int:
+    """E28's NARDownTransform step: fp16 [T, n] -> fp16, H_128 blocks minus (x Y') W''^T."""
+    import numpy as np
+    import torch
+
+    from narhip import ops
+    x_host = torch.from_numpy(w.x.view(np.int16))
+    R = max(2, min(8, -(-2 * MALL_BYTES // max(w.x.nbytes, 1)) + 1))
+    xs = [x_host.to(dev).view(torch.float16) for _ in range(R)]
+    outs = [torch.empty_like(xs[0]) for _ in range(R)]
+    v = torch.from_numpy(w.v).to(dev)
+    wt = torch.from_numpy(w.w_t).to(dev)
+
+    def step(i: int) -> None:
+        ops.transform_f16(xs[i % R], wt, v=v, had_q=128, out=outs[i % R])
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize(dev)
+    stream = torch.cuda.current_stream(dev)
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record(stream)
+    for i in range(args.steps):
+        step(i)
+    ev1.record(stream)
+    torch.cuda.synchronize(dev)
+    wall = time.perf_counter() - t0
+    ms_step = ev0.elapsed_time(ev1) / args.steps
+    t, n = w.tokens, w.n
+    alg_bytes = w.algorithmic_bytes()
+    achieved = alg_bytes / (ms_step * 1e-3) / 1e9
+    line = {
+        "metric": "E28 fp16 down_proj transform (NARDownTransform.forward): tokens/s, 1 MI355X",
+        "value": t / (ms_step * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms_step, "us_per_call": ms_step * 1e3, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (seeded, narhip/workloads.py)",
+        "config": {"workload": f"{w.name}: {t} tokens x {n} fp16, H128 per block, k={w.k}, fp16 out",
+                   "tokens": t, "n": n, "k": w.k, "rotated_buffers": R},
+        "achieved_gbps": achieved, "hbm_frac": achieved / HBM_PEAK_GBPS, "wall_s": wall,
+        "roofline": {"kernel": "transform_f16 call (proj_f64 + fold_f64 + rq_seg fp16)", "bound": "hbm",
+                     "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBPS, "traffic": None},
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline_transform(w, args.cpu_seconds)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def cpu_baseline_transform(w, target_s: float) -> dict:
+    """reference_transform (quarot-llama3/nar_r4_kernel.py:190-202) on the host cores."""
+    import numpy as np
+    import torch
+
+    import nar_r4_kernel as nk
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    y, wt = torch.from_numpy(w.v), torch.from_numpy(w.w_t)
+    x = torch.from_numpy(w.x.view(np.float16))
+
+    def once(r: int) -> float:
+        t0 = time.perf_counter()
+        nk.reference_transform(x[:r], y, wt).half()
+        return time.perf_counter() - t0
+
+    rows = min(w.tokens, 16)
+    once(rows)
+    dt = once(rows)
+    while dt * 6 < target_s and rows < w.tokens:
+        rows = min(w.tokens, rows * 2)
+        dt = once(rows)
+    med = statistics.median([once(rows) for _ in range(5)])
+    return {"value": rows / med, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"first {rows} of {w.tokens} rows, reference_transform in torch fp32 on the CPU, "
+                      "median of 5 after 1 warmup"}
 
 
 if __name__ == "__main__":

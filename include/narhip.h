@@ -158,8 +158,8 @@ int narhip_hadamard_rows(const void *x_bf16, int64_t rows, int64_t n, int64_t ld
  * u comes from `partial` fp32 [tokens, splits*k] (the split partials of
  * narhip_rank_projection_f16, folded in split order; Kernel B alone) or, with
  * partial NULL, is computed here from v fp32 [n, k] (u = RN32(x V), fp64
- * sums) in a workspace of narhip_transform_f16_workspace() bytes.  k = 0:
- * Hadamard blocks only.  Replaces NARDownTransform.forward
+ * sums).  Scratch: a workspace of narhip_transform_f16_workspace() bytes
+ * (enough for either form).  k = 0: Hadamard blocks only.  Replaces NARDownTransform.forward
  * (quarot-llama3/nar_r4_kernel.py:256-275) and launch_kernel_b with its
  * kernels nar_group_transform_kernel / nar_group_transform_tc_kernel
  * (quarot-llama3/nar_r4_kernel.py:56-120, :155-175). */

@@ -10,6 +10,7 @@
 #include "rq_seg.hip"
 #include "dequant.hip"
 #include "hooks.hip"
+#include "transform_f16.hip"
 
 #include <cmath>
 #include <cstdarg>
@@ -859,12 +860,62 @@ int narhip_hadamard_rows(const void *x_bf16, int64_t rows, int64_t n, int64_t ld
     return launch_seg(sa, had_q, 128, RANK_NONE, s);
 }
 
+namespace {
+
+// fp16 transform at q = 128, k <= 8: proj_tok (+ fold_u64) + xform128.
+bool xf_fast(int32_t had_q, int32_t k) { return had_q == 128 && k >= 1 && k <= XF_K; }
+
+// Channel chunks per projection block: the smallest divisor S of n/128 that
+// gives >= 1024 blocks of 64 tokens (all of them when none does).
+int xf_splits(int64_t T, int64_t n)
+{
+    const int64_t nb = n / 128, tiles = (T + 63) / 64;
+    for (int64_t d = 1; d <= nb; d++)
+        if (nb % d == 0 && tiles * d >= 1024) return (int)d;
+    return (int)nb;
+}
+
+size_t xf_v64_bytes(int64_t n) { return align256(sizeof(double) * XF_K * (size_t)n); }
+size_t xf_pd_bytes(int64_t T, int S) { return align256(sizeof(double) * XF_K * (size_t)T * (size_t)S); }
+size_t xf_u64_bytes(int64_t T) { return align256(sizeof(double) * XF_K * (size_t)T); }
+
+int launch_proj_tok(const uint16_t *x, int64_t T, int64_t n, int64_t ldx, const float *v, int k, int S,
+                    double *v64, double *pd, float *pf, hipStream_t s)
+{
+    hipLaunchKernelGGL(v64_kernel, dim3((unsigned)((n * XF_K + 255) / 256)), dim3(256), 0, s, v, n, k, v64);
+    int rc = check_launch("v64_kernel");
+    if (rc) return rc;
+    ProjTokArgs a{x, ldx, T, n, v64, pd, pf, k, S};
+    hipLaunchKernelGGL(proj_tok_kernel, dim3((unsigned)((T + 63) / 64), (unsigned)S), dim3(256), 0, s, a);
+    return check_launch("proj_tok_kernel");
+}
+
+int launch_xform128(const uint16_t *x, int64_t T, int64_t n, int64_t ldx, const float *w_t, const double *u64,
+                    int k, uint16_t *out, hipStream_t s)
+{
+    const int64_t gx = (n / 128 + 15) / 16;
+    int64_t gy = (2048 + gx - 1) / gx;
+    if (gy > T) gy = T;
+    const int64_t tpb = (T + gy - 1) / gy;
+    gy = (T + tpb - 1) / tpb;
+    XformArgs a{x, ldx, T, n, w_t, u64, out, k, (int)tpb, f32_sqrt(128), 0.0f};
+    a.rsq = 1.0f / a.sq;
+    hipLaunchKernelGGL(xform128_kernel, dim3((unsigned)gx, (unsigned)gy), dim3(256), 0, s, a);
+    return check_launch("xform128_kernel");
+}
+
+}  // namespace
+
 size_t narhip_transform_f16_workspace(int64_t tokens, int64_t n, int32_t k)
 {
     if (tokens <= 0 || n <= 0 || k <= 0 || k > 16) return 0;
+    size_t fast = 0;
+    if (k <= XF_K && n % 128 == 0)
+        fast = xf_v64_bytes(n) + xf_pd_bytes(tokens, xf_splits(tokens, n)) + xf_u64_bytes(tokens);
     const int sp = f64_splits(tokens, n);
-    return align256(sizeof(double) * (size_t)tokens * (size_t)sp * (size_t)f64_kmax(k)) +
-           align256(sizeof(float) * (size_t)tokens * (size_t)k);
+    const size_t seg = align256(sizeof(double) * (size_t)tokens * (size_t)sp * (size_t)f64_kmax(k)) +
+                       align256(sizeof(float) * (size_t)tokens * (size_t)k);
+    return fast > seg ? fast : seg;
 }
 
 int narhip_rank_projection_f16(const void *x_f16, int64_t tokens, int64_t n, int64_t ld_x, const float *v,
@@ -894,16 +945,36 @@ int narhip_transform_f16(const void *x_f16, int64_t tokens, int64_t n, int64_t l
     if (k < 0 || k > 16) return fail(NARHIP_EUNSUPPORTED, "fp16 transform supports rank k <= 16 (got %d)", k);
     if (ld_x < n || ld_x % 8) return fail(NARHIP_EINVAL, "ld_x=%lld must be >= n and a multiple of 8", (long long)ld_x);
     if (partial && (splits < 1 || k < 1)) return fail(NARHIP_EINVAL, "partials need splits >= 1 and k >= 1");
-    const size_t need = partial ? 0 : narhip_transform_f16_workspace(tokens, n, k);
-    if (need > 0 && (!workspace || workspace_bytes < need))
-        return fail(NARHIP_EWORKSPACE, "workspace of %zu bytes required, %zu given", need, workspace_bytes);
     if (tokens == 0) return NARHIP_OK;
     if (!x_f16 || !out_f16 || (k > 0 && (!w_t || (!partial && !v)))) return fail(NARHIP_EINVAL, "null tensor argument");
+    const bool fast = xf_fast(had_q, k);
+    const size_t need = partial ? (fast ? xf_u64_bytes(tokens) : 0) : narhip_transform_f16_workspace(tokens, n, k);
+    if (need > 0 && (!workspace || workspace_bytes < need))
+        return fail(NARHIP_EWORKSPACE, "workspace of %zu bytes required, %zu given", need, workspace_bytes);
     if (!aligned16(x_f16) || !aligned16(out_f16) || !aligned16(w_t) || !aligned16(v))
         return fail(NARHIP_EINVAL, "x, out, v and w_t must be 16-byte aligned");
     hipStream_t s = static_cast<hipStream_t>(stream);
     const uint16_t *x = static_cast<const uint16_t *>(x_f16);
     int rc;
+    if (fast) {
+        char *ws = static_cast<char *>(workspace);
+        double *u64;
+        if (partial) {
+            u64 = reinterpret_cast<double *>(ws);
+            hipLaunchKernelGGL(fold_u64_kernel, dim3((unsigned)((tokens * XF_K + 255) / 256)), dim3(256), 0, s,
+                               nullptr, partial, splits, k, tokens, u64);
+        } else {
+            const int S = xf_splits(tokens, n);
+            double *v64 = reinterpret_cast<double *>(ws);
+            double *pd = reinterpret_cast<double *>(ws + xf_v64_bytes(n));
+            u64 = reinterpret_cast<double *>(ws + xf_v64_bytes(n) + xf_pd_bytes(tokens, S));
+            if ((rc = launch_proj_tok(x, tokens, n, ld_x, v, k, S, v64, pd, nullptr, s))) return rc;
+            hipLaunchKernelGGL(fold_u64_kernel, dim3((unsigned)((tokens * XF_K + 255) / 256)), dim3(256), 0, s,
+                               pd, nullptr, S, k, tokens, u64);
+        }
+        if ((rc = check_launch("fold_u64_kernel"))) return rc;
+        return launch_xform128(x, tokens, n, ld_x, w_t, u64, k, static_cast<uint16_t *>(out_f16), s);
+    }
     SegArgs a{};
     a.splits = 1;
     if (partial) {

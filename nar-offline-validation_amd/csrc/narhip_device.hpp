@@ -86,6 +86,50 @@ __device__ __forceinline__ int lane_chunk(int l16)
     return (l0 ^ l2) | ((l1 ^ l2) << 1) | ((l2 ^ l3) << 2) | (l3 << 3);
 }
 
+// FWHT_Q of one segment held by a 16-lane row, NH = Q/128 chunks of 8 values
+// per lane (segment position p = h*128 + chunk*8 + e).  Stages w = 1, 2, 4 are
+// in-register, w = 8..64 one DPP exchange each (lower lane x + p, upper p - x),
+// w >= 128 in-register across h: the stage order of the reference's FWHT
+// (nar/extended_experiment.py:443-456), every stage one fp32 add or subtract.
+template <int NH>
+__device__ __forceinline__ void fwht_row(float (&v)[8 * NH], int chunk)
+{
+#pragma unroll
+    for (int w = 1; w < 8; w <<= 1)
+#pragma unroll
+        for (int h = 0; h < NH; h++)
+#pragma unroll
+            for (int e = 0; e < 8; e++)
+                if (!(e & w)) {
+                    float x0 = v[h * 8 + e], x1 = v[h * 8 + e + w];
+                    v[h * 8 + e] = x0 + x1;
+                    v[h * 8 + e + w] = x0 - x1;
+                }
+    const float s0 = (chunk & 1) ? -1.0f : 1.0f;
+    const float s1 = (chunk & 2) ? -1.0f : 1.0f;
+    const float s2 = (chunk & 4) ? -1.0f : 1.0f;
+    const float s3 = (chunk & 8) ? -1.0f : 1.0f;
+#pragma unroll
+    for (int i = 0; i < 8 * NH; i++) v[i] = __builtin_fmaf(s0, v[i], dpp_f32<DPP_XOR1>(v[i]));
+#pragma unroll
+    for (int i = 0; i < 8 * NH; i++) v[i] = __builtin_fmaf(s1, v[i], dpp_f32<DPP_XOR2>(v[i]));
+#pragma unroll
+    for (int i = 0; i < 8 * NH; i++) v[i] = __builtin_fmaf(s2, v[i], dpp_f32<DPP_XOR7>(v[i]));
+#pragma unroll
+    for (int i = 0; i < 8 * NH; i++) v[i] = __builtin_fmaf(s3, v[i], dpp_f32<DPP_XOR15>(v[i]));
+#pragma unroll
+    for (int wh = 1; wh < NH; wh <<= 1)
+#pragma unroll
+        for (int h = 0; h < NH; h++)
+            if (!(h & wh))
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    float x0 = v[h * 8 + e], x1 = v[(h + wh) * 8 + e];
+                    v[h * 8 + e] = x0 + x1;
+                    v[(h + wh) * 8 + e] = x0 - x1;
+                }
+}
+
 // Sum over the 16 lanes of a row in fp64; every lane receives the identical value.
 __device__ __forceinline__ double row_sum64(double v)
 {

@@ -111,45 +111,8 @@ rq_seg_kernel(SegArgs a)
             for (int e = 0; e < 8; e++) v[h * 8 + e] *= a.signs[base + h * 128 + chunk * 8 + e];
     }
 
-    // ---- FWHT_Q, stages w = 1, 2, 4 (in-register)
-#pragma unroll
-    for (int w = 1; w < 8; w <<= 1)
-#pragma unroll
-        for (int h = 0; h < NH; h++)
-#pragma unroll
-            for (int e = 0; e < 8; e++)
-                if (!(e & w)) {
-                    float x0 = v[h * 8 + e], x1 = v[h * 8 + e + w];
-                    v[h * 8 + e] = x0 + x1;
-                    v[h * 8 + e + w] = x0 - x1;
-                }
-    // stages w = 8, 16, 32, 64 (DPP inside the row): lower lane x+p, upper p-x
-    {
-        const float s0 = (chunk & 1) ? -1.0f : 1.0f;
-        const float s1 = (chunk & 2) ? -1.0f : 1.0f;
-        const float s2 = (chunk & 4) ? -1.0f : 1.0f;
-        const float s3 = (chunk & 8) ? -1.0f : 1.0f;
-#pragma unroll
-        for (int i = 0; i < NV; i++) v[i] = __builtin_fmaf(s0, v[i], xchg<0>(v[i]));
-#pragma unroll
-        for (int i = 0; i < NV; i++) v[i] = __builtin_fmaf(s1, v[i], xchg<1>(v[i]));
-#pragma unroll
-        for (int i = 0; i < NV; i++) v[i] = __builtin_fmaf(s2, v[i], xchg<2>(v[i]));
-#pragma unroll
-        for (int i = 0; i < NV; i++) v[i] = __builtin_fmaf(s3, v[i], xchg<3>(v[i]));
-    }
-    // stages w = 128, 256, ... (in-register across hi)
-#pragma unroll
-    for (int wh = 1; wh < NH; wh <<= 1)
-#pragma unroll
-        for (int h = 0; h < NH; h++)
-            if (!(h & wh))
-#pragma unroll
-                for (int e = 0; e < 8; e++) {
-                    float x0 = v[h * 8 + e], x1 = v[(h + wh) * 8 + e];
-                    v[h * 8 + e] = x0 + x1;
-                    v[(h + wh) * 8 + e] = x0 - x1;
-                }
+    // ---- FWHT_Q
+    fwht_row<NH>(v, chunk);
     // normalisation: fp32 division by fp32(sqrt(Q))
     div_sqrt_q<Q>(v, a.sq, a.rsq);
 

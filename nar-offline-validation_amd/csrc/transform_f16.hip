@@ -1,0 +1,295 @@
+// E28's fp16 down_proj transform at rank k <= 8 (quarot-llama3/nar_r4_kernel.py
+// NARDownTransform): out = fp16( H_128 blocks(x) / fp32(sqrt 128) - RN32(u W^T) ),
+// u = RN32(x V), from fp16 rows.
+//
+// Two streaming passes over x, each organised so that the factor it needs
+// stays on chip for many tokens instead of being re-read per token:
+//
+//   proj_tok_kernel   one lane per token (64 tokens per block), the block's
+//                     channel chunk streamed through LDS in 128-channel tiles
+//                     of x and of a fp64 copy of V (double-buffered, one
+//                     barrier per tile); each V row is read by a whole wave
+//                     at one address (LDS broadcast).  fp64 FMAs, partial
+//                     sums per chunk.
+//   fold_u64_kernel   u = RN32(sum of the chunk partials in chunk order),
+//                     stored as the fp64 value of that fp32 number.
+//   xform128_kernel   one 16-lane row per 128-channel segment, 16 segments per
+//                     block; each lane keeps W^T for its 8 channels in
+//                     registers as fp64 and loops over a range of tokens
+//                     (x prefetched XF_PF tokens ahead, u by scalar loads).  The butterflies, the
+//                     division and the fp64 correction sum are those of the
+//                     segment kernel, so the fp32 values equal its.
+#include "narhip_device.hpp"
+
+namespace narhip {
+
+constexpr int XF_K = 8;             // rank slots held by the kernels below
+
+// V fp32 [n, k] -> fp64 [n, XF_K], ranks >= k zero.
+__global__ void __launch_bounds__(256)
+v64_kernel(const float *v, int64_t n, int k, double *v64)
+{
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n * XF_K) return;
+    const int64_t c = i / XF_K;
+    const int r = (int)(i % XF_K);
+    v64[i] = r < k ? (double)v[c * k + r] : 0.0;
+}
+
+struct ProjTokArgs {
+    const uint16_t *x;        // fp16 rows [T, ldx]
+    int64_t ldx, T, n;
+    const double *v64;        // [n, XF_K]
+    double *pd;               // [T][S][XF_K] fp64 chunk sums, or null
+    float *pf;                // [T][S*k] fp32 chunk sums (each rounded once), or null
+    int k, S;                 // chunk = n / S channels, a multiple of 128
+};
+
+constexpr int PT_TC = 128;                  // channels per LDS tile
+constexpr int PT_ROWB = PT_TC * 2 + 16;     // padded x row (272 B: conflict-free b128 column reads)
+constexpr int PT_XB = 64 * PT_ROWB;         // x tile bytes
+constexpr int PT_VB = PT_TC * XF_K * 8;     // V tile bytes (fp64)
+constexpr int PT_BUF = PT_XB + PT_VB;
+
+__global__ void __launch_bounds__(256, 3)
+proj_tok_kernel(ProjTokArgs a)
+{
+    __shared__ __align__(16) uint8_t lds[2 * PT_BUF];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = tid >> 6;
+    const int64_t t0 = (int64_t)blockIdx.x * 64;
+    const int64_t chunk = a.n / a.S;
+    const int64_t c0 = (int64_t)blockIdx.y * chunk;
+    const int ntiles = (int)(chunk / PT_TC);
+
+    // loader: x -- thread -> token row lr, 64-byte quarter lq of the tile's 256 bytes;
+    //         V -- thread -> 32 contiguous bytes of the tile's 8 KB
+    const int lr = tid >> 2, lq = tid & 3;
+    const int64_t trow = t0 + lr < a.T ? t0 + lr : a.T - 1;
+    const uint4 *xsrc = reinterpret_cast<const uint4 *>(a.x + trow * a.ldx + c0 + lq * 32);
+    const uint4 *vsrc = reinterpret_cast<const uint4 *>(a.v64 + c0 * XF_K) + 2 * tid;
+    const int xoff = lr * PT_ROWB + lq * 64, voff = PT_XB + 32 * tid;
+    uint4 x0 = xsrc[0], x1 = xsrc[1], x2 = xsrc[2], x3 = xsrc[3];
+    uint4 v0 = vsrc[0], v1 = vsrc[1];
+    {
+        uint4 *d = reinterpret_cast<uint4 *>(lds + xoff);
+        d[0] = x0; d[1] = x1; d[2] = x2; d[3] = x3;
+        uint4 *dv = reinterpret_cast<uint4 *>(lds + voff);
+        dv[0] = v0; dv[1] = v1;
+    }
+    __syncthreads();
+
+    double acc[XF_K];
+#pragma unroll
+    for (int r = 0; r < XF_K; r++) acc[r] = 0.0;
+    // the wave's 32 channels of each tile: x by lane = token, V rows broadcast
+    const int xme = lane * PT_ROWB + w * 64;
+    const int vme = PT_XB + w * 32 * XF_K * 8;
+
+    for (int tile = 0; tile < ntiles; tile++) {
+        const uint8_t *buf = lds + (tile & 1) * PT_BUF;
+        // next tile's x and V into registers (the last tile reloads itself), then
+        // into the other buffer after this tile's FMAs: no branches, so the
+        // loads, the FMAs and the stores stay in one schedule region
+        const int tn = tile + 1 < ntiles ? tile + 1 : tile;
+        {
+            const uint4 *xs = xsrc + tn * (PT_TC / 8);
+            const uint4 *vs = vsrc + tn * (PT_VB / 16);
+            x0 = xs[0]; x1 = xs[1]; x2 = xs[2]; x3 = xs[3];
+            v0 = vs[0]; v1 = vs[1];
+        }
+        const uint4 *row = reinterpret_cast<const uint4 *>(buf + xme);
+        const double2 *vt = reinterpret_cast<const double2 *>(buf + vme);
+        uint32_t wd[16];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const uint4 p = row[q];
+            wd[4 * q] = p.x; wd[4 * q + 1] = p.y; wd[4 * q + 2] = p.z; wd[4 * q + 3] = p.w;
+        }
+        // V rows two channels ahead of the FMAs; the fences keep the compiler
+        // from hoisting all 128 row reads of the tile into registers
+        double2 va[XF_K / 2], vb[XF_K / 2];
+#pragma unroll
+        for (int r2 = 0; r2 < XF_K / 2; r2++) {
+            va[r2] = vt[r2];
+            vb[r2] = vt[XF_K / 2 + r2];
+        }
+#pragma unroll
+        for (int c = 0; c < 32; c++) {
+            double2 vc[XF_K / 2];
+#pragma unroll
+            for (int r2 = 0; r2 < XF_K / 2; r2++) {
+                vc[r2] = va[r2];
+                va[r2] = vb[r2];
+            }
+            if (c + 2 < 32) {
+#pragma unroll
+                for (int r2 = 0; r2 < XF_K / 2; r2++) vb[r2] = vt[(c + 2) * (XF_K / 2) + r2];
+            }
+            const uint32_t h = (c & 1) ? (wd[c >> 1] >> 16) : (wd[c >> 1] & 0xffffu);
+            const double xv = (double)f16_bits_to_f32((uint16_t)h);
+#pragma unroll
+            for (int r2 = 0; r2 < XF_K / 2; r2++) {
+                acc[2 * r2] = fma(xv, vc[r2].x, acc[2 * r2]);
+                acc[2 * r2 + 1] = fma(xv, vc[r2].y, acc[2 * r2 + 1]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        {
+            uint8_t *nb = lds + ((tile + 1) & 1) * PT_BUF;
+            uint4 *d = reinterpret_cast<uint4 *>(nb + xoff);
+            d[0] = x0; d[1] = x1; d[2] = x2; d[3] = x3;
+            uint4 *dv = reinterpret_cast<uint4 *>(nb + voff);
+            dv[0] = v0; dv[1] = v1;
+        }
+        __syncthreads();
+    }
+
+    // combine the four waves' channel quarters in wave order
+    double *red = reinterpret_cast<double *>(lds);     // [4][64][XF_K], 16 KB
+#pragma unroll
+    for (int r = 0; r < XF_K; r++) red[(w * 64 + lane) * XF_K + r] = acc[r];
+    __syncthreads();
+    if (w == 0) {
+        const int64_t t = t0 + lane;
+        if (t < a.T) {
+#pragma unroll
+            for (int r = 0; r < XF_K; r++) {
+                double s = red[lane * XF_K + r];
+                s += red[(64 + lane) * XF_K + r];
+                s += red[(128 + lane) * XF_K + r];
+                s += red[(192 + lane) * XF_K + r];
+                if (a.pd) a.pd[(t * a.S + blockIdx.y) * XF_K + r] = s;
+                else if (r < a.k) a.pf[(t * a.S + blockIdx.y) * a.k + r] = (float)s;
+            }
+        }
+    }
+}
+
+// u64[t][r] = (double) RN32( sum over chunks s of pd[t][s][r] ), s in order;
+// or, from fp32 partials [T][S*k], RN32 of their fp64 sum.  Ranks >= k: 0.
+__global__ void __launch_bounds__(256)
+fold_u64_kernel(const double *pd, const float *pf, int S, int k, int64_t T, double *u64)
+{
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= T * XF_K) return;
+    const int64_t t = i / XF_K;
+    const int r = (int)(i % XF_K);
+    double s = 0.0;
+    if (r < k) {
+        if (pd) {
+            for (int c = 0; c < S; c++) s += pd[(t * S + c) * XF_K + r];
+        } else {
+            for (int c = 0; c < S; c++) s += (double)pf[t * S * k + c * k + r];
+        }
+    }
+    u64[i] = (double)(float)s;
+}
+
+struct XformArgs {
+    const uint16_t *x;        // fp16 rows [T, ldx]
+    int64_t ldx, T, n;
+    const float *wt;          // [k, n]
+    const double *u64;        // [T][XF_K]
+    uint16_t *out;            // fp16 [T, n]
+    int k;
+    int tpb;                  // tokens per block (blockIdx.y-th range)
+    float sq, rsq;            // fp32(sqrt 128), RN(1/sq)
+};
+
+__device__ __forceinline__ void f16x8_to_f32(const uint4 p, float (&v)[8])
+{
+    const uint32_t wd[4] = {p.x, p.y, p.z, p.w};
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        v[2 * j] = f16_bits_to_f32((uint16_t)(wd[j] & 0xffffu));
+        v[2 * j + 1] = f16_bits_to_f32((uint16_t)(wd[j] >> 16));
+    }
+}
+
+constexpr int XF_PF = 8;            // x prefetch depth of xform128 (tokens)
+
+// u rows are the same for every lane: read through the constant address space
+// (scalar loads, which do not queue behind the x prefetches).
+typedef const __attribute__((address_space(4))) double cdouble;
+
+__device__ __forceinline__ void xform_token(const XformArgs &a, const double (&W)[XF_K][8], uint4 x,
+                                            int64_t t, int64_t ch, int chunk, bool active)
+{
+    float v[8];
+    f16x8_to_f32(x, v);
+    fwht_row<1>(v, chunk);
+    div_sqrt_q<128>(v, a.sq, a.rsq);
+    cdouble *u = (cdouble *)(a.u64 + t * XF_K);
+    double acc[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) acc[e] = 0.0;
+#pragma unroll
+    for (int r = 0; r < XF_K; r++) {
+        if (r < a.k) {
+            const double ur = u[r];
+#pragma unroll
+            for (int e = 0; e < 8; e++) acc[e] = fma(ur, W[r][e], acc[e]);
+        }
+    }
+    uint32_t o[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const float lo = v[2 * j] - (float)acc[2 * j];
+        const float hi = v[2 * j + 1] - (float)acc[2 * j + 1];
+        o[j] = (uint32_t)f32_to_f16_bits(lo) | ((uint32_t)f32_to_f16_bits(hi) << 16);
+    }
+    if (active) *reinterpret_cast<uint4 *>(a.out + t * a.n + ch) = make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+__global__ void __launch_bounds__(256)
+xform128_kernel(XformArgs a)
+{
+    const int lane = threadIdx.x & 63;
+    const int l16 = lane & 15;
+    const int row = threadIdx.x >> 4;
+    const int64_t nseg = a.n / 128;
+    const int64_t seg = (int64_t)blockIdx.x * 16 + row;
+    const bool active = seg < nseg;
+    const int chunk = lane_chunk(l16);
+    const int64_t ch = (active ? seg : 0) * 128 + chunk * 8;
+
+    // W^T for the lane's 8 channels, fp64
+    double W[XF_K][8];
+#pragma unroll
+    for (int r = 0; r < XF_K; r++) {
+        if (r < a.k) {
+            const float4 *wr = reinterpret_cast<const float4 *>(a.wt + (int64_t)r * a.n + ch);
+            const float4 w0 = wr[0], w1 = wr[1];
+            W[r][0] = w0.x; W[r][1] = w0.y; W[r][2] = w0.z; W[r][3] = w0.w;
+            W[r][4] = w1.x; W[r][5] = w1.y; W[r][6] = w1.z; W[r][7] = w1.w;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; e++) W[r][e] = 0.0;
+        }
+    }
+
+    const int64_t tb = (int64_t)blockIdx.y * a.tpb;
+    const int64_t te = tb + a.tpb < a.T ? tb + a.tpb : a.T;
+    if (tb >= te) return;
+    const uint16_t *xc = a.x + ch;
+    // x rows XF_PF tokens ahead of the arithmetic (loads past te repeat row te-1)
+    uint4 ring[XF_PF];
+#pragma unroll
+    for (int i = 0; i < XF_PF; i++) {
+        const int64_t tl = tb + i < te ? tb + i : te - 1;
+        ring[i] = *reinterpret_cast<const uint4 *>(xc + tl * a.ldx);
+    }
+    for (int64_t t0 = tb; t0 < te; t0 += XF_PF) {
+#pragma unroll
+        for (int i = 0; i < XF_PF; i++) {
+            const int64_t t = t0 + i;
+            const uint4 cur = ring[i];
+            const int64_t tl = t + XF_PF < te ? t + XF_PF : te - 1;
+            ring[i] = *reinterpret_cast<const uint4 *>(xc + tl * a.ldx);
+            if (t < te) xform_token(a, W, cur, t, ch, chunk, active);
+        }
+    }
+}
+
+}  // namespace narhip

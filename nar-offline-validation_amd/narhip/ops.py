@@ -231,7 +231,7 @@ def transform_f16(x: torch.Tensor, w_t: torch.Tensor | None, *, v: torch.Tensor 
     else:
         _require(out, torch.float16, "out", dev)
     lib = _lib.load()
-    ws_bytes = 0 if partial is not None else lib.narhip_transform_f16_workspace(T, n, k)
+    ws_bytes = lib.narhip_transform_f16_workspace(T, n, k)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
     rc = lib.narhip_transform_f16(_p(x), T, n, x.stride(0), had_q, _p(v) if k else None,
                                   _p(partial) if k else None, splits, _p(w_t), k, _p(out), _p(ws), ws_bytes,

@@ -72,10 +72,17 @@ class Workload:
     def k(self) -> int:
         return 0 if self.v is None else int(self.v.shape[1])
 
+    @property
+    def transform_f16(self) -> bool:
+        """E28's fp16-in / fp16-out transform (x holds fp16 bits, no quantizer)."""
+        return self.meta.get("io") == "f16"
+
     def algorithmic_bytes(self) -> int:
-        """T*(2n + n/2 + 4n/b) + factor bytes read once (fp32 U, V)."""
+        """T*(2n + n/2 + 4n/b) + factor bytes read once (fp32 U, V); fp16 transform: T*4n + factors."""
         t, n, b = self.tokens, self.n, self.group
         factors = 0 if self.v is None else self.v.nbytes + self.w_t.nbytes
+        if self.transform_f16:
+            return t * 4 * n + factors
         return t * (2 * n + n // 2 + 4 * n // b) + factors
 
 
@@ -189,6 +196,16 @@ def e17_3b(tokens: int = 2048, k: int = 8) -> Workload:
     return Workload(f"e17_3b_k{k}", bf16_bits(x), (1, 128), 128, v=v, w_t=w_t)
 
 
+def e28(model: str = "8b", tokens: int = 2048, k: int = 8) -> Workload:
+    """E28's down_proj transform (quarot-llama3/nar_r4_kernel.py NARDownTransform): fp16
+    rows of the Llama-3.1-8B (14336) or Llama-3.2-3B (8192) down_proj input, H_128
+    blocks, full-row rank k=8, fp16 out.  SiLU(gate)*up rows with 16 outliers x50."""
+    n = {"8b": 14336, "3b": 8192}[model]
+    x, v, w_t = _e17(10 + (model == "3b"), tokens, n, k, 16)
+    bits = np.asarray(x, dtype=np.float16).view(np.uint16)
+    return Workload(f"e28_{model}_T{tokens}", bits, (1, 128), 128, v=v, w_t=w_t, meta={"io": "f16"})
+
+
 CONFIGS = {
     "kcache_3b": kcache_3b,
     "qproj_3b": qproj_3b,
@@ -203,4 +220,6 @@ REFERENCE_SETTINGS = {
     "e17_8b_k32": lambda: e17_8b(k=32),
     "e17_3b_k8": lambda: e17_3b(k=8),
     "e17_3b_k32": lambda: e17_3b(k=32),
+    "e28_8b": lambda tokens=2048: e28("8b", tokens),
+    "e28_3b": lambda tokens=2048: e28("3b", tokens),
 }
