@@ -38,11 +38,14 @@ MALL_BYTES = 256 << 20
 # counters read a 1 GiB device copy (bench.py --copy-mb 1024) as 1 GiB each way.
 TRAFFIC_SOURCE = "profiles/hbm_traffic.md"
 TRAFFIC_BYTES = {
-    "downproj_8b": 1604.0e6,
-    "downproj_70b": 6302.1e6,
+    "downproj_8b": 1572.4e6,
+    "downproj_70b": 6283.5e6,
     "qproj_3b": 171.5e6,
     "kcache_3b": 5.8e6,
     "vcache_decode_8b": 0.6e6,
+    "e17_8b_k8": 143.4e6,
+    "e28_8b_2048": 208.0e6,
+    "e28_8b_32768": 2900.5e6,
 }
 
 
@@ -199,6 +202,8 @@ def main() -> int:
     kron = w.hadamard[0] > 1
     if full_row_rank and mode != ops.RANK_EXACT and (w.k >= 16 or mode == ops.RANK_MFMA):
         kernels = f"proj_mfma + {'kron_mfma' if kron else 'rq_seg'} + fold_u + corr_quant"
+    elif full_row_rank and mode == ops.RANK_AUTO and not kron:
+        kernels = "proj_f64 + fold_f64 + rq_seg"
     elif full_row_rank:
         kernels = "proj_exact + corr_exact + rq_row" if kron else "proj_exact + rq_seg"
     else:
@@ -266,6 +271,7 @@ def bench_transform_f16(args, w, dev) -> int:
     t, n = w.tokens, w.n
     alg_bytes = w.algorithmic_bytes()
     achieved = alg_bytes / (ms_step * 1e-3) / 1e9
+    traffic = TRAFFIC_BYTES.get(f"{args.config}_{t}")
     line = {
         "metric": "E28 fp16 down_proj transform (NARDownTransform.forward): tokens/s, 1 MI355X",
         "value": t / (ms_step * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
@@ -275,9 +281,10 @@ def bench_transform_f16(args, w, dev) -> int:
         "config": {"workload": f"{w.name}: {t} tokens x {n} fp16, H128 per block, k={w.k}, fp16 out",
                    "tokens": t, "n": n, "k": w.k, "rotated_buffers": R},
         "achieved_gbps": achieved, "hbm_frac": achieved / HBM_PEAK_GBPS, "wall_s": wall,
-        "roofline": {"kernel": "transform_f16 call (proj_f64 + fold_f64 + rq_seg fp16)", "bound": "hbm",
+        "roofline": {"kernel": "transform_f16 call (v64 + proj_tok + fold_u64 + xform128)", "bound": "hbm",
                      "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBPS, "traffic": None},
+                     "frac": achieved / HBM_PEAK_GBPS, "traffic": traffic,
+                     "traffic_source": TRAFFIC_SOURCE if traffic else None},
     }
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline_transform(w, args.cpu_seconds)
