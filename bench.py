@@ -56,9 +56,11 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="downproj_8b",
                     choices=["kcache_3b", "qproj_3b", "downproj_8b", "vcache_decode_8b", "downproj_70b",
-                             "e17_8b_k8", "e17_8b_k32", "e17_3b_k8", "e17_3b_k32", "e28_8b", "e28_3b"])
+                             "e17_8b_k8", "e17_8b_k32", "e17_3b_k8", "e17_3b_k32", "e28_8b", "e28_3b",
+                             "w4a4_8b"])
     ap.add_argument("--tokens", type=int, default=0,
-                    help="token count of the e28_* transform settings (default 2048)")
+                    help="token count of the e28_* transform settings (default 2048) and of w4a4_8b "
+                         "(default 8192)")
     ap.add_argument("--rank-mode", default="auto", choices=["auto", "exact", "mfma"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU baseline work")
@@ -148,6 +150,8 @@ def main() -> int:
     from narhip import ops, workloads
 
     mode = {"auto": ops.RANK_AUTO, "exact": ops.RANK_EXACT, "mfma": ops.RANK_MFMA}[args.rank_mode]
+    if args.config == "w4a4_8b":
+        return bench_w4a4(args, torch.device("cuda:0"))
     if args.config.startswith("e28_"):
         w = workloads.REFERENCE_SETTINGS[args.config](args.tokens or 2048)
     else:
@@ -288,6 +292,55 @@ def bench_transform_f16(args, w, dev) -> int:
     }
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline_transform(w, args.cpu_seconds)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def bench_w4a4(args, dev) -> int:
+    """Group-asymmetric W4A4 GEMM on the Llama-3.1-8B down_proj shape: packed INT4
+    activations [T, 14336] x packed INT4 weights [4096, 14336], fp32 out."""
+    import numpy as np
+    import torch
+
+    from narhip import ops
+    T, n, O = args.tokens or 8192, 14336, 4096
+    rng = np.random.default_rng(20260902)
+    f16 = lambda x: torch.from_numpy(np.asarray(x, np.float16)).to(dev)  # noqa: E731
+    a = torch.from_numpy(rng.integers(0, 256, (T, n // 2), dtype=np.uint8)).to(dev)
+    w = torch.from_numpy(rng.integers(0, 256, (O, n // 2), dtype=np.uint8)).to(dev)
+    sa, za = f16(rng.uniform(0.005, 0.2, (T, n // 128))), f16(rng.uniform(-2, 1, (T, n // 128)))
+    sw, zw = f16(rng.uniform(0.001, 0.02, (O, n // 128))), f16(rng.uniform(-0.1, 0.05, (O, n // 128)))
+    out = torch.empty((T, O), dtype=torch.float32, device=dev)
+
+    def timed(fn, steps, warmup):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize(dev)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize(dev)
+        return e0.elapsed_time(e1) / steps
+
+    ms = timed(lambda: ops.w4a4_gemm(a, sa, za, w, sw, zw, out=out), args.steps, args.warmup)
+    xb = torch.randn((T, n), device=dev, dtype=torch.bfloat16)
+    wb = torch.randn((n, O), device=dev, dtype=torch.bfloat16)
+    ms_bf16 = timed(lambda: torch.mm(xb, wb), args.steps, args.warmup)
+    ops_per = 2.0 * T * O * n
+    achieved = ops_per / (ms * 1e-3) / 1e12
+    line = {
+        "metric": "group-asymmetric W4A4 GEMM (packed INT4 A and W, fp16 scale/zero per 128): tokens/s, 1 MI355X",
+        "value": T / (ms * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+        "data": "synthetic (seeded codes and scales)",
+        "config": {"workload": f"w4a4_8b: {T} x {n} INT4 activations, {O} x {n} INT4 weights, b=128, fp32 out",
+                   "tokens": T, "n": n, "out_features": O},
+        "roofline": {"kernel": "w4a4_kernel", "bound": "mfma", "achieved": achieved, "peak": 5000.0,
+                     "unit": "TOPS", "frac": achieved / 5000.0, "traffic": None},
+        "torch_bf16_mm_ms": ms_bf16,
+    }
     print(json.dumps(line), flush=True)
     return 0
 

@@ -176,6 +176,25 @@ size_t narhip_transform_f16_workspace(int64_t tokens, int64_t n, int32_t k);
 int narhip_rank_projection_f16(const void *x_f16, int64_t tokens, int64_t n, int64_t ld_x, const float *v,
                                int32_t k, int32_t splits, float *partial, void *stream);
 
+/* Group-asymmetric W4A4 GEMM, the consumer of the packed INT4 format:
+ * out[t, o] = sum_i (qA[t,i] sA[t,i/128] + zA[t,i/128]) (qW[o,i] sW[o,i/128] + zW[o,i/128])
+ * for activations (codes uint8 [tokens, n/2], low nibble = even channel; fp16
+ * scales / zeros [tokens, n/128]: the output of narhip_rotate_quant) and
+ * weights in the same format [out_features, ...]; out fp32 [tokens, ld_out].
+ * Per group: integer code products on int8 MFMA, then
+ * sA sW sum qA qW + sA SA zW + zA (sW SW + 128 zW) in fp32 (SA, SW the code
+ * sums).  group must be 128.  With few output tiles (decode) the groups are
+ * split over workgroups and the partials summed in split order.  The reference documents this form and runs no
+ * such GEMM (quarot-llama3/e28_v2/docs/quantizer_contract.md:134-140); it is
+ * the consumer named by the packed layout of nar/kernels/r4_fused_v2.py:80-92. */
+int narhip_w4a4_gemm(const uint8_t *a_codes, const void *a_scales, const void *a_zeros, int64_t tokens,
+                     const uint8_t *w_codes, const void *w_scales, const void *w_zeros, int64_t out_features,
+                     int64_t n, int32_t group, float *out, int64_t ld_out, void *workspace, size_t workspace_bytes,
+                     void *stream);
+/* Scratch bytes narhip_w4a4_gemm needs (0 when the reduction is not split:
+ * split partials [splits][tokens][out_features] fp32 for few output tiles). */
+size_t narhip_w4a4_workspace(int64_t tokens, int64_t out_features, int64_t n);
+
 /* Device self-test of the MFMA operand mapping the kernels rely on (no
  * counterpart in the reference): one v_mfma_f32_16x16x32_bf16 with
  * a_bf16[64*8], b_bf16[64*8] per lane, d[64*4] per lane (device memory). */

@@ -11,6 +11,7 @@
 #include "dequant.hip"
 #include "hooks.hip"
 #include "transform_f16.hip"
+#include "w4a4.hip"
 
 #include <cmath>
 #include <cstdarg>
@@ -1006,6 +1007,66 @@ int narhip_transform_f16(const void *x_f16, int64_t tokens, int64_t n, int64_t l
     }
 #undef NARHIP_F16_SEG
     return check_launch("rq_seg_kernel (fp16)");
+}
+
+namespace {
+// Reduction splits of the W4A4 GEMM: enough workgroups for the 256 CUs when
+// the output tiles alone are few (decode), at least two groups per split.
+int w4a4_splits(int64_t tokens, int64_t out_features, int64_t n)
+{
+    const int64_t tiles = ((out_features + WQ_TN - 1) / WQ_TN) * ((tokens + WQ_TM - 1) / WQ_TM);
+    const int64_t G = n / 128;
+    int64_t s = 1;
+    while (tiles * s * 2 <= 512 && G / (s * 2) >= 2) s *= 2;
+    return (int)s;
+}
+}  // namespace
+
+size_t narhip_w4a4_workspace(int64_t tokens, int64_t out_features, int64_t n)
+{
+    if (tokens <= 0 || out_features <= 0 || n <= 0 || n % 128) return 0;
+    const int s = w4a4_splits(tokens, out_features, n);
+    return s == 1 ? 0 : sizeof(float) * (size_t)s * (size_t)tokens * (size_t)out_features;
+}
+
+int narhip_w4a4_gemm(const uint8_t *a_codes, const void *a_scales, const void *a_zeros, int64_t tokens,
+                     const uint8_t *w_codes, const void *w_scales, const void *w_zeros, int64_t out_features,
+                     int64_t n, int32_t group, float *out, int64_t ld_out, void *workspace, size_t workspace_bytes,
+                     void *stream)
+{
+    g_error.clear();
+    if (tokens < 0 || out_features < 0 || n <= 0)
+        return fail(NARHIP_EINVAL, "bad shape tokens=%lld out_features=%lld n=%lld", (long long)tokens,
+                    (long long)out_features, (long long)n);
+    if (group != 128) return fail(NARHIP_EUNSUPPORTED, "W4A4 GEMM is built for groups of 128 (got %d)", group);
+    if (n % 128) return fail(NARHIP_EINVAL, "n=%lld is not a multiple of the group size", (long long)n);
+    if (ld_out < out_features) return fail(NARHIP_EINVAL, "ld_out=%lld < out_features", (long long)ld_out);
+    if (tokens == 0 || out_features == 0) return NARHIP_OK;
+    if (!a_codes || !a_scales || !a_zeros || !w_codes || !w_scales || !w_zeros || !out)
+        return fail(NARHIP_EINVAL, "null tensor argument");
+    if (!aligned16(a_codes) || !aligned16(w_codes) || (reinterpret_cast<uintptr_t>(a_scales) |
+        reinterpret_cast<uintptr_t>(a_zeros) | reinterpret_cast<uintptr_t>(w_scales) |
+        reinterpret_cast<uintptr_t>(w_zeros) | reinterpret_cast<uintptr_t>(out)) & 3u)
+        return fail(NARHIP_EINVAL, "codes must be 16-byte aligned, scales, zeros and out 4-byte aligned");
+    const int64_t gx = (out_features + WQ_TN - 1) / WQ_TN, gy = (tokens + WQ_TM - 1) / WQ_TM;
+    if (gy > 65535) return fail(NARHIP_EUNSUPPORTED, "too many tokens for one launch");
+    const int splits = w4a4_splits(tokens, out_features, n);
+    const size_t need = narhip_w4a4_workspace(tokens, out_features, n);
+    if (need && (!workspace || workspace_bytes < need || !aligned16(workspace)))
+        return fail(NARHIP_EWORKSPACE, "workspace of %zu bytes (16-byte aligned) required, %zu given", need,
+                    workspace_bytes);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    float *part = splits == 1 ? out : static_cast<float *>(workspace);
+    W4A4Args a{a_codes, static_cast<const uint16_t *>(a_scales), static_cast<const uint16_t *>(a_zeros), tokens,
+               w_codes, static_cast<const uint16_t *>(w_scales), static_cast<const uint16_t *>(w_zeros),
+               out_features, n, part, ld_out, splits};
+    hipLaunchKernelGGL(w4a4_kernel, dim3((unsigned)gx, (unsigned)gy, (unsigned)splits), dim3(256), 0, s, a);
+    int rc = check_launch("w4a4_kernel");
+    if (rc || splits == 1) return rc;
+    const int64_t cnt = tokens * out_features;
+    hipLaunchKernelGGL(w4a4_reduce_kernel, dim3((unsigned)((cnt + 255) / 256)), dim3(256), 0, s, part, splits, tokens,
+                       out_features, out, ld_out);
+    return check_launch("w4a4_reduce_kernel");
 }
 
 int narhip_mfma_probe(const void *a_bf16, const void *b_bf16, float *d, void *stream)

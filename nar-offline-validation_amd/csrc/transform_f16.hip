@@ -178,7 +178,17 @@ fold_u64_kernel(const double *pd, const float *pf, int S, int k, int64_t T, doub
     double s = 0.0;
     if (r < k) {
         if (pd) {
-            for (int c = 0; c < S; c++) s += pd[(t * S + c) * XF_K + r];
+            // eight independent loads in flight per step, added in chunk order
+            const double *p = pd + t * S * XF_K + r;
+            int c = 0;
+            for (; c + 8 <= S; c += 8) {
+                double v[8];
+#pragma unroll
+                for (int j = 0; j < 8; j++) v[j] = p[(c + j) * XF_K];
+#pragma unroll
+                for (int j = 0; j < 8; j++) s += v[j];
+            }
+            for (; c < S; c++) s += p[c * XF_K];
         } else {
             for (int c = 0; c < S; c++) s += (double)pf[t * S * k + c * k + r];
         }

@@ -240,6 +240,48 @@ def transform_f16(x: torch.Tensor, w_t: torch.Tensor | None, *, v: torch.Tensor 
     return out
 
 
+def pack_codes(codes: torch.Tensor) -> torch.Tensor:
+    """Unpacked codes uint8 [..., n] (0..15) -> packed [..., n/2], low nibble = even channel."""
+    if codes.dtype != torch.uint8 or codes.shape[-1] % 2:
+        raise ValueError("codes must be uint8 with an even last dimension")
+    return (codes[..., 0::2] | (codes[..., 1::2] << 4)).contiguous()
+
+
+def w4a4_gemm(a_codes: torch.Tensor, a_scales: torch.Tensor, a_zeros: torch.Tensor,
+              w_codes: torch.Tensor, w_scales: torch.Tensor, w_zeros: torch.Tensor, *,
+              group: int = 128, out: torch.Tensor | None = None) -> torch.Tensor:
+    """fp32 [T, O] = dequant(A) @ dequant(W)^T for two packed INT4 operands (group-asymmetric).
+
+    a_codes uint8 [T, n/2], a_scales / a_zeros fp16 [T, n/group]; w_* likewise
+    with O rows (weights quantized along their input dimension).
+    """
+    dev = a_codes.device
+    if not a_codes.is_cuda:
+        raise ValueError("operands must be GPU tensors")
+    T, half = a_codes.shape
+    O = w_codes.shape[0]
+    n = 2 * half
+    for t, dt, shape, name in ((a_codes, torch.uint8, (T, half), "a_codes"), (w_codes, torch.uint8, (O, half), "w_codes"),
+                               (a_scales, torch.float16, (T, n // group), "a_scales"),
+                               (a_zeros, torch.float16, (T, n // group), "a_zeros"),
+                               (w_scales, torch.float16, (O, n // group), "w_scales"),
+                               (w_zeros, torch.float16, (O, n // group), "w_zeros")):
+        _require(t, dt, name, dev)
+        if tuple(t.shape) != shape:
+            raise ValueError(f"{name} must be {shape}, got {tuple(t.shape)}")
+    if out is None:
+        out = torch.empty((T, O), dtype=torch.float32, device=dev)
+    else:
+        _require(out, torch.float32, "out", dev)
+    lib = _lib.load()
+    ws_bytes = lib.narhip_w4a4_workspace(T, O, n)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
+    rc = lib.narhip_w4a4_gemm(_p(a_codes), _p(a_scales), _p(a_zeros), T, _p(w_codes), _p(w_scales),
+                              _p(w_zeros), O, n, group, _p(out), out.stride(0), _p(ws), ws_bytes, _stream(dev))
+    _lib.check(rc)
+    return out
+
+
 def group_quant(x: torch.Tensor, partial: torch.Tensor | None, w_t: torch.Tensor | None,
                 codes: torch.Tensor, scales: torch.Tensor, zeros: torch.Tensor, *,
                 hadamard: tuple[int, int] = (1, 128), group: int = 128,

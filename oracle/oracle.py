@@ -273,3 +273,29 @@ def relative_l2(obs: np.ndarray, ref: np.ndarray) -> float:
 
 def sqrt_f32(q: int) -> np.float32:
     return np.float32(math.sqrt(q))
+
+
+def w4a4_gemm(a_packed: np.ndarray, a_s: np.ndarray, a_z: np.ndarray, w_packed: np.ndarray,
+              w_s: np.ndarray, w_z: np.ndarray, n: int, b: int = 128) -> np.ndarray:
+    """fp64 [T, O] = dequant(A) dequant(W)^T: each operand dequantized as the
+    reference's dequantize does (fp32 q * s, then + z; nar/kernels/r4_fused_v2.py:
+    364-369), the products summed exactly in fp64.  The group-asymmetric GEMM the
+    packed format feeds (quarot-llama3/e28_v2/docs/quantizer_contract.md:134-140)."""
+    da = dequant(a_packed, a_s, a_z, n, b).astype(np.float64)
+    dw = dequant(w_packed, w_s, w_z, n, b).astype(np.float64)
+    return da @ dw.T
+
+
+def w4a4_group_formula(a_packed: np.ndarray, a_s: np.ndarray, a_z: np.ndarray, w_packed: np.ndarray,
+                       w_s: np.ndarray, w_z: np.ndarray, n: int, b: int = 128) -> np.ndarray:
+    """The same product from the per-group four-term form, exact in fp64:
+    sum_g sA sW sum qA qW + sA zW sum qA + zA sW sum qW + b zA zW."""
+    qa = unpack(a_packed, n).astype(np.int64).reshape(a_packed.shape[0], n // b, b)
+    qw = unpack(w_packed, n).astype(np.int64).reshape(w_packed.shape[0], n // b, b)
+    sa, za = f16_bits_to_f32(a_s).astype(np.float64), f16_bits_to_f32(a_z).astype(np.float64)
+    sw, zw = f16_bits_to_f32(w_s).astype(np.float64), f16_bits_to_f32(w_z).astype(np.float64)
+    dot = np.einsum("tgj,ogj->tog", qa, qw).astype(np.float64)
+    sum_a, sum_w = qa.sum(-1).astype(np.float64), qw.sum(-1).astype(np.float64)
+    y = (np.einsum("tg,og,tog->to", sa, sw, dot) + np.einsum("tg,og,tg->to", sa, zw, sum_a)
+         + np.einsum("tg,og,og->to", za, sw, sum_w) + b * np.einsum("tg,og->to", za, zw))
+    return y
