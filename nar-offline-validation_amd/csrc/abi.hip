@@ -481,17 +481,77 @@ int64_t chunk_tokens(int64_t T, int64_t n)
     return tc < T ? tc : T;
 }
 
+// fp16 transform at q = 128, k <= 8: proj_tok (+ fold_u64) + xform128.
+bool xf_fast(int32_t had_q, int32_t k) { return had_q == 128 && k >= 1 && k <= XF_K; }
+
+// Channel chunks per projection block: the smallest divisor S of n/128 that
+// gives >= 512 blocks of 64 tokens (all of them when none does; measured:
+// 512 rather than 1024 saves 5 us at 2048 x 14336).
+int xf_splits(int64_t T, int64_t n)
+{
+    const int64_t nb = n / 128, tiles = (T + 63) / 64;
+    for (int64_t d = 1; d <= nb; d++)
+        if (nb % d == 0 && tiles * d >= 512) return (int)d;
+    return (int)nb;
+}
+
+size_t xf_v64_bytes(int64_t n) { return align256(sizeof(double) * XF_K * (size_t)n); }
+size_t xf_pd_bytes(int64_t T, int S) { return align256(sizeof(double) * XF_K * (size_t)T * (size_t)S); }
+size_t xf_u64_bytes(int64_t T) { return align256(sizeof(double) * XF_K * (size_t)T); }
+
+int launch_proj_tok(const uint16_t *x, int64_t T, int64_t n, int64_t ldx, const float *v, int k, int S,
+                    double *v64, double *pd, float *pf, hipStream_t s, bool f16 = true)
+{
+    hipLaunchKernelGGL(v64_kernel, dim3((unsigned)((n * XF_K + 255) / 256)), dim3(256), 0, s, v, n, k, v64);
+    int rc = check_launch("v64_kernel");
+    if (rc) return rc;
+    ProjTokArgs a{x, ldx, T, n, v64, pd, pf, k, S};
+    const dim3 grid((unsigned)((T + 63) / 64), (unsigned)S);
+    if (f16) hipLaunchKernelGGL(proj_tok_kernel<true>, grid, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL(proj_tok_kernel<false>, grid, dim3(256), 0, s, a);
+    return check_launch("proj_tok_kernel");
+}
+
+// quant != null: bf16 rows, INT4 group-128 outputs (codes, scales, zeros, dest
+// and signs from *quant); else fp16 rows to fp16 `out`.
+int launch_xform128(const uint16_t *x, int64_t T, int64_t n, int64_t ldx, const float *w_t, const double *u64,
+                    int k, uint16_t *out, hipStream_t s, const XformArgs *quant = nullptr)
+{
+    // ~2048 workgroups, but at least 32 tokens each (each loads 64 KB of W^T
+    // before its first token) while that still leaves >= 512 workgroups
+    const int64_t gx = (n / 128 + 15) / 16;
+    int64_t gy = (2048 + gx - 1) / gx;
+    if (T < 32 * gy) {
+        const int64_t lo = (512 + gx - 1) / gx;
+        gy = (T + 31) / 32 > lo ? (T + 31) / 32 : lo;
+    }
+    if (gy > T) gy = T;
+    const int64_t tpb = (T + gy - 1) / gy;
+    gy = (T + tpb - 1) / tpb;
+    XformArgs a = quant ? *quant : XformArgs{};
+    a.x = x; a.ldx = ldx; a.T = T; a.n = n; a.wt = w_t; a.u64 = u64; a.out = out; a.k = k; a.tpb = (int)tpb;
+    a.sq = f32_sqrt(128);
+    a.rsq = 1.0f / a.sq;
+    const dim3 grid((unsigned)gx, (unsigned)gy);
+    if (quant) hipLaunchKernelGGL(xform128_kernel<true>, grid, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL(xform128_kernel<false>, grid, dim3(256), 0, s, a);
+    return check_launch("xform128_kernel");
+}
+
+
 struct Plan {
     Path path;
     bool kron;
     int seg_mode;
     bool need_prep, need_proj, need_P, need_corr, vproj;
+    bool xf;          // block-H_128, k <= 8: proj_tok + fold_u64 + xform128 (group 128, no rotated output)
     int splits;
     int64_t chunk;
-    size_t prep_b, proj_b, P_b, corr_b, u_b;
+    size_t prep_b, proj_b, P_b, corr_b, u_b, xf_b;
     size_t total() const
     {
-        return align256(prep_b) + align256(proj_b) + align256(P_b) + align256(corr_b) + align256(u_b);
+        const size_t sum = align256(prep_b) + align256(proj_b) + align256(P_b) + align256(corr_b) + align256(u_b);
+        return xf_b > sum ? xf_b : sum;
     }
 };
 
@@ -558,6 +618,11 @@ int make_plan(int64_t T, int64_t n, int m, int q, int k, int64_t nb, bool have_p
     } else {
         p.path = PATH_SEG_PARTIAL_EXACT;
         p.seg_mode = RANK_PARTIAL;
+        if (!exact && q == 128 && xf_fast(q, k)) {
+            p.xf = true;
+            p.xf_b = have_partial ? xf_u64_bytes(T)
+                                  : xf_v64_bytes(n) + xf_pd_bytes(T, xf_splits(T, n)) + xf_u64_bytes(T);
+        }
     }
     return NARHIP_OK;
 }
@@ -650,6 +715,32 @@ int run_rotate_quant(const void *x_bf16, int64_t T, int64_t n, int64_t ldx, int 
         return NARHIP_OK;
     }
 
+    if (p.xf && group == 128 && !rotated) {
+        // u as fp64 of RN32(sum), W^T for the lane's channels held in registers
+        char *w0 = static_cast<char *>(ws);
+        double *u64;
+        if (partial) {
+            u64 = reinterpret_cast<double *>(w0);
+            hipLaunchKernelGGL(fold_u64_kernel, dim3((unsigned)((T * XF_K + 255) / 256)), dim3(256), 0, s, nullptr,
+                               partial, splits, k, T, u64);
+        } else {
+            const int S = xf_splits(T, n);
+            double *v64 = reinterpret_cast<double *>(w0);
+            double *pd = reinterpret_cast<double *>(w0 + xf_v64_bytes(n));
+            u64 = reinterpret_cast<double *>(w0 + xf_v64_bytes(n) + xf_pd_bytes(T, S));
+            if ((rc = launch_proj_tok(x, T, n, ldx, v, k, S, v64, pd, nullptr, s, false))) return rc;
+            hipLaunchKernelGGL(fold_u64_kernel, dim3((unsigned)((T * XF_K + 255) / 256)), dim3(256), 0, s, pd,
+                               nullptr, S, k, T, u64);
+        }
+        if ((rc = check_launch("fold_u64_kernel"))) return rc;
+        XformArgs qa{};
+        qa.signs = signs;
+        qa.codes = codes;
+        qa.scales = static_cast<uint16_t *>(scales);
+        qa.zeros = static_cast<uint16_t *>(zeros);
+        qa.dest = dest;
+        return launch_xform128(x, T, n, ldx, wt, u64, k, nullptr, s, &qa);
+    }
     const float *part = partial;
     int sp = splits;
     float *uf = reinterpret_cast<float *>(u3);
@@ -861,51 +952,6 @@ int narhip_hadamard_rows(const void *x_bf16, int64_t rows, int64_t n, int64_t ld
     return launch_seg(sa, had_q, 128, RANK_NONE, s);
 }
 
-namespace {
-
-// fp16 transform at q = 128, k <= 8: proj_tok (+ fold_u64) + xform128.
-bool xf_fast(int32_t had_q, int32_t k) { return had_q == 128 && k >= 1 && k <= XF_K; }
-
-// Channel chunks per projection block: the smallest divisor S of n/128 that
-// gives >= 1024 blocks of 64 tokens (all of them when none does).
-int xf_splits(int64_t T, int64_t n)
-{
-    const int64_t nb = n / 128, tiles = (T + 63) / 64;
-    for (int64_t d = 1; d <= nb; d++)
-        if (nb % d == 0 && tiles * d >= 1024) return (int)d;
-    return (int)nb;
-}
-
-size_t xf_v64_bytes(int64_t n) { return align256(sizeof(double) * XF_K * (size_t)n); }
-size_t xf_pd_bytes(int64_t T, int S) { return align256(sizeof(double) * XF_K * (size_t)T * (size_t)S); }
-size_t xf_u64_bytes(int64_t T) { return align256(sizeof(double) * XF_K * (size_t)T); }
-
-int launch_proj_tok(const uint16_t *x, int64_t T, int64_t n, int64_t ldx, const float *v, int k, int S,
-                    double *v64, double *pd, float *pf, hipStream_t s)
-{
-    hipLaunchKernelGGL(v64_kernel, dim3((unsigned)((n * XF_K + 255) / 256)), dim3(256), 0, s, v, n, k, v64);
-    int rc = check_launch("v64_kernel");
-    if (rc) return rc;
-    ProjTokArgs a{x, ldx, T, n, v64, pd, pf, k, S};
-    hipLaunchKernelGGL(proj_tok_kernel, dim3((unsigned)((T + 63) / 64), (unsigned)S), dim3(256), 0, s, a);
-    return check_launch("proj_tok_kernel");
-}
-
-int launch_xform128(const uint16_t *x, int64_t T, int64_t n, int64_t ldx, const float *w_t, const double *u64,
-                    int k, uint16_t *out, hipStream_t s)
-{
-    const int64_t gx = (n / 128 + 15) / 16;
-    int64_t gy = (2048 + gx - 1) / gx;
-    if (gy > T) gy = T;
-    const int64_t tpb = (T + gy - 1) / gy;
-    gy = (T + tpb - 1) / tpb;
-    XformArgs a{x, ldx, T, n, w_t, u64, out, k, (int)tpb, f32_sqrt(128), 0.0f};
-    a.rsq = 1.0f / a.sq;
-    hipLaunchKernelGGL(xform128_kernel, dim3((unsigned)gx, (unsigned)gy), dim3(256), 0, s, a);
-    return check_launch("xform128_kernel");
-}
-
-}  // namespace
 
 size_t narhip_transform_f16_workspace(int64_t tokens, int64_t n, int32_t k)
 {

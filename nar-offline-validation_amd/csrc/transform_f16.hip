@@ -1,6 +1,10 @@
-// E28's fp16 down_proj transform at rank k <= 8 (quarot-llama3/nar_r4_kernel.py
-// NARDownTransform): out = fp16( H_128 blocks(x) / fp32(sqrt 128) - RN32(u W^T) ),
-// u = RN32(x V), from fp16 rows.
+// Block-H_128 rows with a full-row rank term of k <= 8:
+//   E28's fp16 down_proj transform (quarot-llama3/nar_r4_kernel.py
+//   NARDownTransform): out = fp16( H_128 blocks(x) / fp32(sqrt 128) - RN32(u W^T) ),
+//   u = RN32(x V), from fp16 rows;
+//   E17's block-H_128 rotate-and-quantize (nar/kernels/r4_fused_v3.py launch_nar
+//   at k = 8): the same x' from bf16 rows, then the group-128 INT4 quantizer
+//   (each 128-channel segment is one group).
 //
 // Two streaming passes over x, each organised so that the factor it needs
 // stays on chip for many tokens instead of being re-read per token:
@@ -37,7 +41,7 @@ v64_kernel(const float *v, int64_t n, int k, double *v64)
 }
 
 struct ProjTokArgs {
-    const uint16_t *x;        // fp16 rows [T, ldx]
+    const uint16_t *x;        // fp16 (or bf16) rows [T, ldx]
     int64_t ldx, T, n;
     const double *v64;        // [n, XF_K]
     double *pd;               // [T][S][XF_K] fp64 chunk sums, or null
@@ -51,6 +55,7 @@ constexpr int PT_XB = 64 * PT_ROWB;         // x tile bytes
 constexpr int PT_VB = PT_TC * XF_K * 8;     // V tile bytes (fp64)
 constexpr int PT_BUF = PT_XB + PT_VB;
 
+template <bool F16>
 __global__ void __launch_bounds__(256, 3)
 proj_tok_kernel(ProjTokArgs a)
 {
@@ -126,8 +131,13 @@ proj_tok_kernel(ProjTokArgs a)
 #pragma unroll
                 for (int r2 = 0; r2 < XF_K / 2; r2++) vb[r2] = vt[(c + 2) * (XF_K / 2) + r2];
             }
-            const uint32_t h = (c & 1) ? (wd[c >> 1] >> 16) : (wd[c >> 1] & 0xffffu);
-            const double xv = (double)f16_bits_to_f32((uint16_t)h);
+            double xv;
+            if constexpr (F16) {
+                const uint32_t h = (c & 1) ? (wd[c >> 1] >> 16) : (wd[c >> 1] & 0xffffu);
+                xv = (double)f16_bits_to_f32((uint16_t)h);
+            } else {
+                xv = (double)((c & 1) ? bf16hi(wd[c >> 1]) : bf16lo(wd[c >> 1]));
+            }
 #pragma unroll
             for (int r2 = 0; r2 < XF_K / 2; r2++) {
                 acc[2 * r2] = fma(xv, vc[r2].x, acc[2 * r2]);
@@ -197,14 +207,19 @@ fold_u64_kernel(const double *pd, const float *pf, int S, int k, int64_t T, doub
 }
 
 struct XformArgs {
-    const uint16_t *x;        // fp16 rows [T, ldx]
+    const uint16_t *x;        // fp16 rows [T, ldx] (QUANT: bf16)
     int64_t ldx, T, n;
     const float *wt;          // [k, n]
     const double *u64;        // [T][XF_K]
-    uint16_t *out;            // fp16 [T, n]
+    uint16_t *out;            // fp16 [T, n] (transform form)
     int k;
     int tpb;                  // tokens per block (blockIdx.y-th range)
     float sq, rsq;            // fp32(sqrt 128), RN(1/sq)
+    // QUANT form: groups of 128 = one segment
+    const float *signs;       // [n] or null (applied to x before the transform)
+    uint8_t *codes;           // [rows, n/2]
+    uint16_t *scales, *zeros; // [rows, n/128]
+    const int64_t *dest;      // [T] output row per token, or null
 };
 
 __device__ __forceinline__ void f16x8_to_f32(const uint4 p, float (&v)[8])
@@ -223,11 +238,21 @@ constexpr int XF_PF = 8;            // x prefetch depth of xform128 (tokens)
 // (scalar loads, which do not queue behind the x prefetches).
 typedef const __attribute__((address_space(4))) double cdouble;
 
-__device__ __forceinline__ void xform_token(const XformArgs &a, const double (&W)[XF_K][8], uint4 x,
-                                            int64_t t, int64_t ch, int chunk, bool active)
+template <bool QUANT>
+__device__ __forceinline__ void xform_token(const XformArgs &a, const double (&W)[XF_K][8], const float (&sg)[8],
+                                            uint4 x, int64_t t, int64_t ch, int chunk, bool active)
 {
     float v[8];
-    f16x8_to_f32(x, v);
+    if constexpr (QUANT) {
+        v[0] = bf16lo(x.x); v[1] = bf16hi(x.x); v[2] = bf16lo(x.y); v[3] = bf16hi(x.y);
+        v[4] = bf16lo(x.z); v[5] = bf16hi(x.z); v[6] = bf16lo(x.w); v[7] = bf16hi(x.w);
+        if (a.signs) {
+#pragma unroll
+            for (int e = 0; e < 8; e++) v[e] *= sg[e];
+        }
+    } else {
+        f16x8_to_f32(x, v);
+    }
     fwht_row<1>(v, chunk);
     div_sqrt_q<128>(v, a.sq, a.rsq);
     cdouble *u = (cdouble *)(a.u64 + t * XF_K);
@@ -242,16 +267,34 @@ __device__ __forceinline__ void xform_token(const XformArgs &a, const double (&W
             for (int e = 0; e < 8; e++) acc[e] = fma(ur, W[r][e], acc[e]);
         }
     }
-    uint32_t o[4];
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const float lo = v[2 * j] - (float)acc[2 * j];
-        const float hi = v[2 * j + 1] - (float)acc[2 * j + 1];
-        o[j] = (uint32_t)f32_to_f16_bits(lo) | ((uint32_t)f32_to_f16_bits(hi) << 16);
+    for (int e = 0; e < 8; e++) v[e] = v[e] - (float)acc[e];
+    if constexpr (QUANT) {
+        // the segment is one group of 128: min/max over the row, then the codes
+        float lo = v[0], hi = v[0];
+#pragma unroll
+        for (int e = 1; e < 8; e++) { lo = fminf(lo, v[e]); hi = fmaxf(hi, v[e]); }
+        group_minmax<16>(lo, hi);
+        const GroupParams g = group_params(lo, hi);
+        const uint32_t word = quant_word8(v, g);
+        if (active) {
+            const int64_t orow = a.dest ? a.dest[t] : t;
+            *reinterpret_cast<uint32_t *>(a.codes + orow * (a.n / 2) + ch / 2) = word;
+            if (chunk == 0) {
+                a.scales[orow * (a.n / 128) + ch / 128] = g.s16;
+                a.zeros[orow * (a.n / 128) + ch / 128] = g.z16;
+            }
+        }
+    } else {
+        uint32_t o[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            o[j] = (uint32_t)f32_to_f16_bits(v[2 * j]) | ((uint32_t)f32_to_f16_bits(v[2 * j + 1]) << 16);
+        if (active) *reinterpret_cast<uint4 *>(a.out + t * a.n + ch) = make_uint4(o[0], o[1], o[2], o[3]);
     }
-    if (active) *reinterpret_cast<uint4 *>(a.out + t * a.n + ch) = make_uint4(o[0], o[1], o[2], o[3]);
 }
 
+template <bool QUANT>
 __global__ void __launch_bounds__(256)
 xform128_kernel(XformArgs a)
 {
@@ -279,6 +322,16 @@ xform128_kernel(XformArgs a)
         }
     }
 
+    float sg[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) sg[e] = 1.0f;
+    if (QUANT && a.signs) {
+        const float4 *sp = reinterpret_cast<const float4 *>(a.signs + ch);
+        const float4 s0 = sp[0], s1 = sp[1];
+        sg[0] = s0.x; sg[1] = s0.y; sg[2] = s0.z; sg[3] = s0.w;
+        sg[4] = s1.x; sg[5] = s1.y; sg[6] = s1.z; sg[7] = s1.w;
+    }
+
     const int64_t tb = (int64_t)blockIdx.y * a.tpb;
     const int64_t te = tb + a.tpb < a.T ? tb + a.tpb : a.T;
     if (tb >= te) return;
@@ -297,7 +350,7 @@ xform128_kernel(XformArgs a)
             const uint4 cur = ring[i];
             const int64_t tl = t + XF_PF < te ? t + XF_PF : te - 1;
             ring[i] = *reinterpret_cast<const uint4 *>(xc + tl * a.ldx);
-            if (t < te) xform_token(a, W, cur, t, ch, chunk, active);
+            if (t < te) xform_token<QUANT>(a, W, sg, cur, t, ch, chunk, active);
         }
     }
 }
