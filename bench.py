@@ -43,9 +43,9 @@ TRAFFIC_BYTES = {
     "qproj_3b": 171.5e6,
     "kcache_3b": 5.8e6,
     "vcache_decode_8b": 0.6e6,
-    "e17_8b_k8": 143.4e6,
-    "e28_8b_2048": 208.0e6,
-    "e28_8b_32768": 2900.5e6,
+    "e17_8b_k8": 152.7e6,
+    "e28_8b_2048": 195.6e6,
+    "e28_8b_32768": 2896.1e6,
 }
 
 
