@@ -37,6 +37,14 @@ MALL_BYTES = 256 << 20
 # FETCH_SIZE scaled by 2.0 and WRITE_SIZE by 1.0 -- the factors that make the
 # counters read a 1 GiB device copy (bench.py --copy-mb 1024) as 1 GiB each way.
 TRAFFIC_SOURCE = "profiles/hbm_traffic.md"
+# MFMA busy fraction of the rank-k kernels (SQ_VALU_MFMA_BUSY_CYCLES over 1024 SIMDs x the kernel's
+# cycles, profiles/mfma_utilisation.md), for the workloads on the MFMA rank path.
+MFMA_UTIL_SOURCE = "profiles/mfma_utilisation.md"
+MFMA_UTIL = {
+    "qproj_3b": {"proj_mfma": 0.028, "corr_quant": 0.065},
+    "downproj_8b": {"proj_mfma": 0.134, "corr_quant": 0.126},
+    "downproj_70b": {"proj_mfma": 0.271, "corr_quant": 0.287},
+}
 TRAFFIC_BYTES = {
     "downproj_8b": 1572.4e6,
     "downproj_70b": 6283.5e6,
@@ -235,6 +243,8 @@ def main() -> int:
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBPS,
                      "traffic": traffic, "traffic_source": TRAFFIC_SOURCE if traffic else None},
     }
+    if args.config in MFMA_UTIL and mode == ops.RANK_AUTO:
+        line["rank_stage_mfma_busy"] = dict(MFMA_UTIL[args.config], source=MFMA_UTIL_SOURCE)
     if w.dest_rows is not None:
         line["us_per_call"] = ms_step * 1e3
     if not args.no_cpu_baseline:
