@@ -193,3 +193,18 @@ def test_select_configs_then_module():
     torch.cuda.synchronize()
     worst, _ = f16_ulp_report(out, O.rotate(x.float().numpy(), 1, 128, v=y, wt=w))
     assert worst <= 1
+
+
+@pytest.mark.parametrize("k,q", [(12, 128), (16, 128), (8, 256), (4, 1024)])
+def test_transform_segment_kernel_forms(k, q):
+    """Ranks 9..16 and Hadamard blocks wider than 128 run on the segment kernel's fp16 form."""
+    print(f"[test_transform_segment_kernel_forms] k={k} q={q}", flush=True)
+    n = 8192
+    y, w = factors(n, k=k, seed=k + q)
+    x = rows(45, n, seed=k)
+    out = ops.transform_f16(x.cuda(), torch.from_numpy(w).cuda(), v=torch.from_numpy(y).cuda(), had_q=q)
+    torch.cuda.synchronize()
+    ref = O.rotate(x.float().numpy(), 1, q, v=y, wt=w)
+    worst, frac = f16_ulp_report(out, ref)
+    print(f"  max ulp {worst}, differing fraction {frac:.2e}", flush=True)
+    assert worst <= 1 and frac <= 1e-4
