@@ -715,7 +715,7 @@ int run_rotate_quant(const void *x_bf16, int64_t T, int64_t n, int64_t ldx, int 
         return NARHIP_OK;
     }
 
-    if (p.xf && group == 128 && !rotated) {
+    if (p.xf && group == 128 && !rotated && aligned16(signs)) {
         // u as fp64 of RN32(sum), W^T for the lane's channels held in registers
         char *w0 = static_cast<char *>(ws);
         double *u64;

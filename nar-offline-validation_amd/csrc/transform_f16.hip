@@ -19,10 +19,11 @@
 //                     stored as the fp64 value of that fp32 number.
 //   xform128_kernel   one 16-lane row per 128-channel segment, 16 segments per
 //                     block; each lane keeps W^T for its 8 channels in
-//                     registers as fp64 and loops over a range of tokens
-//                     (x prefetched XF_PF tokens ahead, u by scalar loads).  The butterflies, the
-//                     division and the fp64 correction sum are those of the
-//                     segment kernel, so the fp32 values equal its.
+//                     registers as fp64 and loops over a range of tokens (x
+//                     prefetched XF_PF tokens ahead, u by scalar loads).  The
+//                     butterflies, the division and the fp64 correction sum are
+//                     those of the segment kernel, so the fp32 values equal its;
+//                     then fp16 out, or (QUANT) the group-128 INT4 quantizer.
 #include "narhip_device.hpp"
 
 namespace narhip {
