@@ -295,7 +295,7 @@ def bench_transform_f16(args, w, dev) -> int:
         "config": {"workload": f"{w.name}: {t} tokens x {n} fp16, H128 per block, k={w.k}, fp16 out",
                    "tokens": t, "n": n, "k": w.k, "rotated_buffers": R},
         "achieved_gbps": achieved, "hbm_frac": achieved / HBM_PEAK_GBPS, "wall_s": wall,
-        "roofline": {"kernel": "transform_f16 call (v64 + proj_tok + fold_u64 + xform128)", "bound": "hbm",
+        "roofline": {"kernel": "transform_f16 call (proj_tok + xform128)", "bound": "hbm",
                      "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBPS, "traffic": traffic,
                      "traffic_source": TRAFFIC_SOURCE if traffic else None},

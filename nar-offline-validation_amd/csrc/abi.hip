@@ -481,7 +481,8 @@ int64_t chunk_tokens(int64_t T, int64_t n)
     return tc < T ? tc : T;
 }
 
-// fp16 transform at q = 128, k <= 8: proj_tok (+ fold_u64) + xform128.
+// fp16 transform at q = 128, k <= 8: proj_tok (unless the caller brings
+// partials) + xform128, which folds the chunk sums itself.
 bool xf_fast(int32_t had_q, int32_t k) { return had_q == 128 && k >= 1 && k <= XF_K; }
 
 // Channel chunks per projection block: the smallest divisor S of n/128 that
@@ -495,27 +496,23 @@ int xf_splits(int64_t T, int64_t n)
     return (int)nb;
 }
 
-size_t xf_v64_bytes(int64_t n) { return align256(sizeof(double) * XF_K * (size_t)n); }
 size_t xf_pd_bytes(int64_t T, int S) { return align256(sizeof(double) * XF_K * (size_t)T * (size_t)S); }
-size_t xf_u64_bytes(int64_t T) { return align256(sizeof(double) * XF_K * (size_t)T); }
 
 int launch_proj_tok(const uint16_t *x, int64_t T, int64_t n, int64_t ldx, const float *v, int k, int S,
-                    double *v64, double *pd, float *pf, hipStream_t s, bool f16 = true)
+                    double *pd, float *pf, hipStream_t s, bool f16 = true)
 {
-    hipLaunchKernelGGL(v64_kernel, dim3((unsigned)((n * XF_K + 255) / 256)), dim3(256), 0, s, v, n, k, v64);
-    int rc = check_launch("v64_kernel");
-    if (rc) return rc;
-    ProjTokArgs a{x, ldx, T, n, v64, pd, pf, k, S};
+    ProjTokArgs a{x, ldx, T, n, v, pd, pf, k, S};
     const dim3 grid((unsigned)((T + 63) / 64), (unsigned)S);
     if (f16) hipLaunchKernelGGL(proj_tok_kernel<true>, grid, dim3(256), 0, s, a);
     else hipLaunchKernelGGL(proj_tok_kernel<false>, grid, dim3(256), 0, s, a);
     return check_launch("proj_tok_kernel");
 }
 
-// quant != null: bf16 rows, INT4 group-128 outputs (codes, scales, zeros, dest
-// and signs from *quant); else fp16 rows to fp16 `out`.
-int launch_xform128(const uint16_t *x, int64_t T, int64_t n, int64_t ldx, const float *w_t, const double *u64,
-                    int k, uint16_t *out, hipStream_t s, const XformArgs *quant = nullptr)
+// u from proj_tok's chunk sums pd [T][S][XF_K], or from the caller's fp32
+// partials pf [T][S*k].  quant != null: bf16 rows, INT4 group-128 outputs
+// (codes, scales, zeros, dest and signs from *quant); else fp16 rows to fp16 `out`.
+int launch_xform128(const uint16_t *x, int64_t T, int64_t n, int64_t ldx, const float *w_t, const double *pd,
+                    const float *pf, int S, int k, uint16_t *out, hipStream_t s, const XformArgs *quant = nullptr)
 {
     // ~2048 workgroups, but at least 32 tokens each (each loads 64 KB of W^T
     // before its first token) while that still leaves >= 512 workgroups
@@ -529,7 +526,7 @@ int launch_xform128(const uint16_t *x, int64_t T, int64_t n, int64_t ldx, const 
     const int64_t tpb = (T + gy - 1) / gy;
     gy = (T + tpb - 1) / tpb;
     XformArgs a = quant ? *quant : XformArgs{};
-    a.x = x; a.ldx = ldx; a.T = T; a.n = n; a.wt = w_t; a.u64 = u64; a.out = out; a.k = k; a.tpb = (int)tpb;
+    a.x = x; a.ldx = ldx; a.T = T; a.n = n; a.wt = w_t; a.pd = pd; a.pf = pf; a.S = S; a.out = out; a.k = k; a.tpb = (int)tpb;
     a.sq = f32_sqrt(128);
     a.rsq = 1.0f / a.sq;
     const dim3 grid((unsigned)gx, (unsigned)gy);
@@ -544,7 +541,7 @@ struct Plan {
     bool kron;
     int seg_mode;
     bool need_prep, need_proj, need_P, need_corr, vproj;
-    bool xf;          // block-H_128, k <= 8: proj_tok + fold_u64 + xform128 (group 128, no rotated output)
+    bool xf;          // block-H_128, k <= 8: proj_tok + xform128 (group 128, no rotated output)
     int splits;
     int64_t chunk;
     size_t prep_b, proj_b, P_b, corr_b, u_b, xf_b;
@@ -620,8 +617,7 @@ int make_plan(int64_t T, int64_t n, int m, int q, int k, int64_t nb, bool have_p
         p.seg_mode = RANK_PARTIAL;
         if (!exact && q == 128 && xf_fast(q, k)) {
             p.xf = true;
-            p.xf_b = have_partial ? xf_u64_bytes(T)
-                                  : xf_v64_bytes(n) + xf_pd_bytes(T, xf_splits(T, n)) + xf_u64_bytes(T);
+            p.xf_b = have_partial ? 0 : xf_pd_bytes(T, xf_splits(T, n));
         }
     }
     return NARHIP_OK;
@@ -717,29 +713,20 @@ int run_rotate_quant(const void *x_bf16, int64_t T, int64_t n, int64_t ldx, int 
 
     if (p.xf && group == 128 && !rotated && aligned16(signs)) {
         // u as fp64 of RN32(sum), W^T for the lane's channels held in registers
-        char *w0 = static_cast<char *>(ws);
-        double *u64;
-        if (partial) {
-            u64 = reinterpret_cast<double *>(w0);
-            hipLaunchKernelGGL(fold_u64_kernel, dim3((unsigned)((T * XF_K + 255) / 256)), dim3(256), 0, s, nullptr,
-                               partial, splits, k, T, u64);
-        } else {
-            const int S = xf_splits(T, n);
-            double *v64 = reinterpret_cast<double *>(w0);
-            double *pd = reinterpret_cast<double *>(w0 + xf_v64_bytes(n));
-            u64 = reinterpret_cast<double *>(w0 + xf_v64_bytes(n) + xf_pd_bytes(T, S));
-            if ((rc = launch_proj_tok(x, T, n, ldx, v, k, S, v64, pd, nullptr, s, false))) return rc;
-            hipLaunchKernelGGL(fold_u64_kernel, dim3((unsigned)((T * XF_K + 255) / 256)), dim3(256), 0, s, pd,
-                               nullptr, S, k, T, u64);
+        double *pd = nullptr;
+        int S = splits;
+        if (!partial) {
+            S = xf_splits(T, n);
+            pd = static_cast<double *>(ws);
+            if ((rc = launch_proj_tok(x, T, n, ldx, v, k, S, pd, nullptr, s, false))) return rc;
         }
-        if ((rc = check_launch("fold_u64_kernel"))) return rc;
         XformArgs qa{};
         qa.signs = signs;
         qa.codes = codes;
         qa.scales = static_cast<uint16_t *>(scales);
         qa.zeros = static_cast<uint16_t *>(zeros);
         qa.dest = dest;
-        return launch_xform128(x, T, n, ldx, wt, u64, k, nullptr, s, &qa);
+        return launch_xform128(x, T, n, ldx, wt, pd, partial, S, k, nullptr, s, &qa);
     }
     const float *part = partial;
     int sp = splits;
@@ -958,7 +945,7 @@ size_t narhip_transform_f16_workspace(int64_t tokens, int64_t n, int32_t k)
     if (tokens <= 0 || n <= 0 || k <= 0 || k > 16) return 0;
     size_t fast = 0;
     if (k <= XF_K && n % 128 == 0)
-        fast = xf_v64_bytes(n) + xf_pd_bytes(tokens, xf_splits(tokens, n)) + xf_u64_bytes(tokens);
+        fast = xf_pd_bytes(tokens, xf_splits(tokens, n));
     const int sp = f64_splits(tokens, n);
     const size_t seg = align256(sizeof(double) * (size_t)tokens * (size_t)sp * (size_t)f64_kmax(k)) +
                        align256(sizeof(float) * (size_t)tokens * (size_t)k);
@@ -995,7 +982,7 @@ int narhip_transform_f16(const void *x_f16, int64_t tokens, int64_t n, int64_t l
     if (tokens == 0) return NARHIP_OK;
     if (!x_f16 || !out_f16 || (k > 0 && (!w_t || (!partial && !v)))) return fail(NARHIP_EINVAL, "null tensor argument");
     const bool fast = xf_fast(had_q, k);
-    const size_t need = partial ? (fast ? xf_u64_bytes(tokens) : 0) : narhip_transform_f16_workspace(tokens, n, k);
+    const size_t need = partial ? 0 : narhip_transform_f16_workspace(tokens, n, k);
     if (need > 0 && (!workspace || workspace_bytes < need))
         return fail(NARHIP_EWORKSPACE, "workspace of %zu bytes required, %zu given", need, workspace_bytes);
     if (!aligned16(x_f16) || !aligned16(out_f16) || !aligned16(w_t) || !aligned16(v))
@@ -1004,23 +991,14 @@ int narhip_transform_f16(const void *x_f16, int64_t tokens, int64_t n, int64_t l
     const uint16_t *x = static_cast<const uint16_t *>(x_f16);
     int rc;
     if (fast) {
-        char *ws = static_cast<char *>(workspace);
-        double *u64;
-        if (partial) {
-            u64 = reinterpret_cast<double *>(ws);
-            hipLaunchKernelGGL(fold_u64_kernel, dim3((unsigned)((tokens * XF_K + 255) / 256)), dim3(256), 0, s,
-                               nullptr, partial, splits, k, tokens, u64);
-        } else {
-            const int S = xf_splits(tokens, n);
-            double *v64 = reinterpret_cast<double *>(ws);
-            double *pd = reinterpret_cast<double *>(ws + xf_v64_bytes(n));
-            u64 = reinterpret_cast<double *>(ws + xf_v64_bytes(n) + xf_pd_bytes(tokens, S));
-            if ((rc = launch_proj_tok(x, tokens, n, ld_x, v, k, S, v64, pd, nullptr, s))) return rc;
-            hipLaunchKernelGGL(fold_u64_kernel, dim3((unsigned)((tokens * XF_K + 255) / 256)), dim3(256), 0, s,
-                               pd, nullptr, S, k, tokens, u64);
+        double *pd = nullptr;
+        int S = splits;
+        if (!partial) {
+            S = xf_splits(tokens, n);
+            pd = static_cast<double *>(workspace);
+            if ((rc = launch_proj_tok(x, tokens, n, ld_x, v, k, S, pd, nullptr, s))) return rc;
         }
-        if ((rc = check_launch("fold_u64_kernel"))) return rc;
-        return launch_xform128(x, tokens, n, ld_x, w_t, u64, k, static_cast<uint16_t *>(out_f16), s);
+        return launch_xform128(x, tokens, n, ld_x, w_t, pd, partial, S, k, static_cast<uint16_t *>(out_f16), s);
     }
     SegArgs a{};
     a.splits = 1;

@@ -11,16 +11,17 @@
 //
 //   proj_tok_kernel   one lane per token (64 tokens per block), the block's
 //                     channel chunk streamed through LDS in 128-channel tiles
-//                     of x and of a fp64 copy of V (double-buffered, one
-//                     barrier per tile); each V row is read by a whole wave
-//                     at one address (LDS broadcast).  fp64 FMAs, partial
-//                     sums per chunk.
-//   fold_u64_kernel   u = RN32(sum of the chunk partials in chunk order),
-//                     stored as the fp64 value of that fp32 number.
+//                     of x and of V (converted to fp64 as it is staged;
+//                     double-buffered, one barrier per tile); each V row is
+//                     read by a whole wave at one address (LDS broadcast).
+//                     fp64 FMAs; fp64 sums per channel chunk, or, with one
+//                     chunk, u = RN32(sum) itself.
 //   xform128_kernel   one 16-lane row per 128-channel segment, 16 segments per
 //                     block; each lane keeps W^T for its 8 channels in
 //                     registers as fp64 and loops over a range of tokens (x
-//                     prefetched XF_PF tokens ahead, u by scalar loads).  The
+//                     prefetched XF_PF tokens ahead).  u comes by scalar loads:
+//                     as stored, or RN32 of the chunk sums (or of the caller's
+//                     fp32 partials) added in chunk order.  The
 //                     butterflies, the division and the fp64 correction sum are
 //                     those of the segment kernel, so the fp32 values equal its;
 //                     then fp16 out, or (QUANT) the group-128 INT4 quantizer.
@@ -30,22 +31,11 @@ namespace narhip {
 
 constexpr int XF_K = 8;             // rank slots held by the kernels below
 
-// V fp32 [n, k] -> fp64 [n, XF_K], ranks >= k zero.
-__global__ void __launch_bounds__(256)
-v64_kernel(const float *v, int64_t n, int k, double *v64)
-{
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= n * XF_K) return;
-    const int64_t c = i / XF_K;
-    const int r = (int)(i % XF_K);
-    v64[i] = r < k ? (double)v[c * k + r] : 0.0;
-}
-
 struct ProjTokArgs {
     const uint16_t *x;        // fp16 (or bf16) rows [T, ldx]
     int64_t ldx, T, n;
-    const double *v64;        // [n, XF_K]
-    double *pd;               // [T][S][XF_K] fp64 chunk sums, or null
+    const float *v;           // V [n, k]
+    double *pd;               // [T][S][XF_K] fp64 chunk sums (S == 1: RN32 of the sum), or null
     float *pf;                // [T][S*k] fp32 chunk sums (each rounded once), or null
     int k, S;                 // chunk = n / S channels, a multiple of 128
 };
@@ -69,19 +59,31 @@ proj_tok_kernel(ProjTokArgs a)
     const int ntiles = (int)(chunk / PT_TC);
 
     // loader: x -- thread -> token row lr, 64-byte quarter lq of the tile's 256 bytes;
-    //         V -- thread -> 32 contiguous bytes of the tile's 8 KB
+    //         V -- thread -> tile elements 4 tid .. 4 tid + 3 of [128 channels][XF_K ranks]
+    //         (rank slots >= k are 0), stored as fp64
     const int lr = tid >> 2, lq = tid & 3;
     const int64_t trow = t0 + lr < a.T ? t0 + lr : a.T - 1;
     const uint4 *xsrc = reinterpret_cast<const uint4 *>(a.x + trow * a.ldx + c0 + lq * 32);
-    const uint4 *vsrc = reinterpret_cast<const uint4 *>(a.v64 + c0 * XF_K) + 2 * tid;
+    const int vc = (4 * tid) / XF_K, vr = (4 * tid) % XF_K;    // channel in the tile, first rank slot
+    const float *vsrc = a.v + (c0 + vc) * a.k;
     const int xoff = lr * PT_ROWB + lq * 64, voff = PT_XB + 32 * tid;
+    float vf[4];
+    auto load_v = [&](int tile) {
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            vf[j] = vr + j < a.k ? vsrc[(int64_t)tile * PT_TC * a.k + vr + j] : 0.0f;
+    };
+    auto store_v = [&](uint8_t *buf) {
+        double2 *dv = reinterpret_cast<double2 *>(buf + voff);
+        dv[0] = make_double2((double)vf[0], (double)vf[1]);
+        dv[1] = make_double2((double)vf[2], (double)vf[3]);
+    };
     uint4 x0 = xsrc[0], x1 = xsrc[1], x2 = xsrc[2], x3 = xsrc[3];
-    uint4 v0 = vsrc[0], v1 = vsrc[1];
+    load_v(0);
     {
         uint4 *d = reinterpret_cast<uint4 *>(lds + xoff);
         d[0] = x0; d[1] = x1; d[2] = x2; d[3] = x3;
-        uint4 *dv = reinterpret_cast<uint4 *>(lds + voff);
-        dv[0] = v0; dv[1] = v1;
+        store_v(lds);
     }
     __syncthreads();
 
@@ -100,9 +102,8 @@ proj_tok_kernel(ProjTokArgs a)
         const int tn = tile + 1 < ntiles ? tile + 1 : tile;
         {
             const uint4 *xs = xsrc + tn * (PT_TC / 8);
-            const uint4 *vs = vsrc + tn * (PT_VB / 16);
             x0 = xs[0]; x1 = xs[1]; x2 = xs[2]; x3 = xs[3];
-            v0 = vs[0]; v1 = vs[1];
+            load_v(tn);
         }
         const uint4 *row = reinterpret_cast<const uint4 *>(buf + xme);
         const double2 *vt = reinterpret_cast<const double2 *>(buf + vme);
@@ -150,8 +151,7 @@ proj_tok_kernel(ProjTokArgs a)
             uint8_t *nb = lds + ((tile + 1) & 1) * PT_BUF;
             uint4 *d = reinterpret_cast<uint4 *>(nb + xoff);
             d[0] = x0; d[1] = x1; d[2] = x2; d[3] = x3;
-            uint4 *dv = reinterpret_cast<uint4 *>(nb + voff);
-            dv[0] = v0; dv[1] = v1;
+            store_v(nb);
         }
         __syncthreads();
     }
@@ -170,48 +170,20 @@ proj_tok_kernel(ProjTokArgs a)
                 s += red[(64 + lane) * XF_K + r];
                 s += red[(128 + lane) * XF_K + r];
                 s += red[(192 + lane) * XF_K + r];
-                if (a.pd) a.pd[(t * a.S + blockIdx.y) * XF_K + r] = s;
+                if (a.pd) a.pd[(t * a.S + blockIdx.y) * XF_K + r] = a.S == 1 ? (double)(float)s : s;
                 else if (r < a.k) a.pf[(t * a.S + blockIdx.y) * a.k + r] = (float)s;
             }
         }
     }
 }
 
-// u64[t][r] = (double) RN32( sum over chunks s of pd[t][s][r] ), s in order;
-// or, from fp32 partials [T][S*k], RN32 of their fp64 sum.  Ranks >= k: 0.
-__global__ void __launch_bounds__(256)
-fold_u64_kernel(const double *pd, const float *pf, int S, int k, int64_t T, double *u64)
-{
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= T * XF_K) return;
-    const int64_t t = i / XF_K;
-    const int r = (int)(i % XF_K);
-    double s = 0.0;
-    if (r < k) {
-        if (pd) {
-            // eight independent loads in flight per step, added in chunk order
-            const double *p = pd + t * S * XF_K + r;
-            int c = 0;
-            for (; c + 8 <= S; c += 8) {
-                double v[8];
-#pragma unroll
-                for (int j = 0; j < 8; j++) v[j] = p[(c + j) * XF_K];
-#pragma unroll
-                for (int j = 0; j < 8; j++) s += v[j];
-            }
-            for (; c < S; c++) s += p[c * XF_K];
-        } else {
-            for (int c = 0; c < S; c++) s += (double)pf[t * S * k + c * k + r];
-        }
-    }
-    u64[i] = (double)(float)s;
-}
-
 struct XformArgs {
     const uint16_t *x;        // fp16 rows [T, ldx] (QUANT: bf16)
     int64_t ldx, T, n;
     const float *wt;          // [k, n]
-    const double *u64;        // [T][XF_K]
+    const double *pd;         // u: proj_tok's [T][S][XF_K] (S == 1: already RN32), or null
+    const float *pf;          // u: caller's fp32 partials [T][S*k] (used when pd is null)
+    int S;
     uint16_t *out;            // fp16 [T, n] (transform form)
     int k;
     int tpb;                  // tokens per block (blockIdx.y-th range)
@@ -235,13 +207,39 @@ __device__ __forceinline__ void f16x8_to_f32(const uint4 p, float (&v)[8])
 
 constexpr int XF_PF = 8;            // x prefetch depth of xform128 (tokens)
 
-// u rows are the same for every lane: read through the constant address space
-// (scalar loads, which do not queue behind the x prefetches).
-typedef const __attribute__((address_space(4))) double cdouble;
+constexpr int XF_UW = 32;           // tokens per u window (one fold pass of the block)
+static_assert(XF_UW * XF_K == 256 && XF_UW % XF_PF == 0, "u window: one (token, rank) per thread");
+
+// u[t][r] as the fp64 value of an fp32 number: RN32 of the chunk sums added in
+// chunk order (proj_tok's fp64 sums, already rounded when there is one chunk,
+// or the caller's fp32 partials).  Ranks >= k: 0.
+__device__ __forceinline__ double fold_u(const XformArgs &a, int64_t t, int r)
+{
+    if (r >= a.k) return 0.0;
+    double s = 0.0;
+    if (a.pd) {
+        const double *p = a.pd + t * a.S * XF_K + r;
+        if (a.S == 1) return p[0];
+        int c = 0;
+        for (; c + 16 <= a.S; c += 16) {      // sixteen loads in flight, added in order
+            double v[16];
+#pragma unroll
+            for (int j = 0; j < 16; j++) v[j] = p[(c + j) * XF_K];
+#pragma unroll
+            for (int j = 0; j < 16; j++) s += v[j];
+        }
+        for (; c < a.S; c++) s += p[c * XF_K];
+    } else {
+        const float *p = a.pf + t * a.S * a.k + r;
+        for (int c = 0; c < a.S; c++) s += (double)p[c * a.k];
+    }
+    return (double)(float)s;
+}
 
 template <bool QUANT>
 __device__ __forceinline__ void xform_token(const XformArgs &a, const double (&W)[XF_K][8], const float (&sg)[8],
-                                            uint4 x, int64_t t, int64_t ch, int chunk, bool active)
+                                            const double *ut, uint4 x, int64_t t, int64_t ch, int chunk,
+                                            bool active)
 {
     float v[8];
     if constexpr (QUANT) {
@@ -256,7 +254,15 @@ __device__ __forceinline__ void xform_token(const XformArgs &a, const double (&W
     }
     fwht_row<1>(v, chunk);
     div_sqrt_q<128>(v, a.sq, a.rsq);
-    cdouble *u = (cdouble *)(a.u64 + t * XF_K);
+    double u[XF_K];
+    {
+        const double2 *u2 = reinterpret_cast<const double2 *>(ut);     // one LDS address per wave
+#pragma unroll
+        for (int r = 0; r < XF_K / 2; r++) {
+            const double2 d = u2[r];
+            u[2 * r] = d.x; u[2 * r + 1] = d.y;
+        }
+    }
     double acc[8];
 #pragma unroll
     for (int e = 0; e < 8; e++) acc[e] = 0.0;
@@ -333,6 +339,7 @@ xform128_kernel(XformArgs a)
         sg[4] = s1.x; sg[5] = s1.y; sg[6] = s1.z; sg[7] = s1.w;
     }
 
+    __shared__ double ubuf[2][XF_UW][XF_K];
     const int64_t tb = (int64_t)blockIdx.y * a.tpb;
     const int64_t te = tb + a.tpb < a.T ? tb + a.tpb : a.T;
     if (tb >= te) return;
@@ -344,14 +351,25 @@ xform128_kernel(XformArgs a)
         const int64_t tl = tb + i < te ? tb + i : te - 1;
         ring[i] = *reinterpret_cast<const uint4 *>(xc + tl * a.ldx);
     }
-    for (int64_t t0 = tb; t0 < te; t0 += XF_PF) {
+    // windows of XF_UW tokens: the block folds their u into LDS (thread ->
+    // token, rank), then every row reads them; two buffers, one barrier each
+    for (int64_t w0 = tb, wi = 0; w0 < te; w0 += XF_UW, wi++) {
+        double (*ub)[XF_K] = ubuf[wi & 1];
+        {
+            const int i = threadIdx.x / XF_K, r = threadIdx.x % XF_K;
+            ub[i][r] = w0 + i < te ? fold_u(a, w0 + i, r) : 0.0;
+        }
+        __syncthreads();
+        const int64_t we = w0 + XF_UW < te ? w0 + XF_UW : te;
+        for (int64_t t0 = w0; t0 < we; t0 += XF_PF) {
 #pragma unroll
-        for (int i = 0; i < XF_PF; i++) {
-            const int64_t t = t0 + i;
-            const uint4 cur = ring[i];
-            const int64_t tl = t + XF_PF < te ? t + XF_PF : te - 1;
-            ring[i] = *reinterpret_cast<const uint4 *>(xc + tl * a.ldx);
-            if (t < te) xform_token<QUANT>(a, W, sg, cur, t, ch, chunk, active);
+            for (int i = 0; i < XF_PF; i++) {
+                const int64_t t = t0 + i;
+                const uint4 cur = ring[i];
+                const int64_t tl = t + XF_PF < te ? t + XF_PF : te - 1;
+                ring[i] = *reinterpret_cast<const uint4 *>(xc + tl * a.ldx);
+                if (t < we) xform_token<QUANT>(a, W, sg, ub[t - w0], cur, t, ch, chunk, active);
+            }
         }
     }
 }

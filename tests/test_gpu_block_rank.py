@@ -1,5 +1,5 @@
 """GPU parity of the block-H_128, full-row k <= 8, group-128 rotate-quant path
-(proj_tok + fold_u64 + xform128 with the INT4 epilogue: E17's k = 8 setting).
+(proj_tok + xform128 with the INT4 epilogue: E17's k = 8 setting).
 
 Called without a rotated output (which selects these kernels), against the
 oracle's rotate + quantizer with the tie-aware contract of the MFMA tests at a
