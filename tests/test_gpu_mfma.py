@@ -90,9 +90,18 @@ def test_full_size_mfma_sampled(name):
     print(f"[test_full_size_mfma_sampled] {name}", flush=True)
     w = workloads.CONFIGS[name]()
     codes, scales, zeros, rot = run_mfma(w)
+    # seeded rows, the first and last tiles, and both sides of every 2048-token
+    # boundary (the transform / correction overlap splits the tokens there)
+    edges = [e for b in range(2048, w.tokens, 2048) for e in (b - 1, b)]
     rows = np.unique(np.concatenate([np.random.default_rng(3).choice(w.tokens, size=24, replace=False),
-                                     [0, 63, 64, w.tokens - 1]]))
+                                     [0, 63, 64, w.tokens - 1], edges]))
     check_contract(w, codes, scales, zeros, rot, rows=rows, label=f"{name} rows {len(rows)}")
+    # without the rotated output (the other correction kernel): identical outputs
+    x, v, wt = to_dev_bf16(w.x), to_dev_f32(w.v), to_dev_f32(w.w_t)
+    c2, s2, z2 = ops.rotate_quant(x, hadamard=w.hadamard, v=v, w_t=wt, rank_block=w.rank_block, group=w.group)
+    torch.cuda.synchronize()
+    assert np.array_equal(c2.cpu().numpy(), codes)
+    assert np.array_equal(f16_bits(s2), scales) and np.array_equal(f16_bits(z2), zeros)
 
 
 def test_prepared_factors_give_identical_outputs():
