@@ -57,20 +57,26 @@ kron_mfma_kernel(KronArgs a)
     const int row = tid >> 4;
     const int chunk = lane_chunk(l16);
 
-    // Paley rows as the MFMA A operand
+    // Paley rows as the MFMA A operand, lane l's fragment at hat[mt][l]: built
+    // by wave 0 only (the lane-indexed table lookup is a select chain) and read
+    // by every wave after the first barrier
     const int lane = tid & 63, wv = tid >> 6;
     const int g = lane >> 4, c16 = lane & 15;
-    bf16x8 ha[NMT];
+    __shared__ __align__(16) bf16x8 hat[NMT][64];
+    if (wv == 0) {
 #pragma unroll
-    for (int mt = 0; mt < NMT; mt++) {
-        const int r = 16 * mt + c16;
-        const uint32_t negbits = r < M ? a.paley.neg[r] : 0u;
+        for (int mt = 0; mt < NMT; mt++) {
+            const int r = 16 * mt + c16;
+            const uint32_t negbits = r < M ? a.paley.neg[r] : 0u;
+            bf16x8 h;
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const int c = 8 * g + j;
-            float e = 0.0f;
-            if (r < M && c < M) e = ((negbits >> c) & 1u) ? -1.0f : 1.0f;
-            ha[mt][j] = (__bf16)e;
+            for (int j = 0; j < 8; j++) {
+                const int c = 8 * g + j;
+                float e = 0.0f;
+                if (r < M && c < M) e = ((negbits >> c) & 1u) ? -1.0f : 1.0f;
+                h[j] = (__bf16)e;
+            }
+            hat[mt][lane] = h;
         }
     }
 
@@ -154,6 +160,9 @@ kron_mfma_kernel(KronArgs a)
 
     // ---- phase 2: Paley product on MFMA, one 16-column block at a time, in place
     {
+        bf16x8 ha[NMT];
+#pragma unroll
+        for (int mt = 0; mt < NMT; mt++) ha[mt] = hat[mt][lane];
         const float hm = a.hm;
         constexpr int CB = Q / 16;
         for (int cb = wv; cb < CB; cb += NW) {
@@ -187,14 +196,19 @@ kron_mfma_kernel(KronArgs a)
         const int a = i / (Q / 4);
         return a * (QS / 4) + ((i % (Q / 4)) ^ (fsw(a) >> 2));
     };
+    // row `row` copies segment row `row`: lane l16 moves float4 l16 + 16 j
+    // (256 contiguous bytes per 16 lanes and instruction; the swizzle only flips
+    // bit 2 of the float4 index, so every offset is a constant)
+    auto copy_row = [&](float *dst_row) {
+        const float4 *src = F4 + row * (QS / 4) + (l16 ^ (fsw(row) >> 2));
+        float4 *dst = reinterpret_cast<float4 *>(dst_row + row * Q) + l16;
+#pragma unroll
+        for (int j = 0; j < Q / 64; j++) dst[16 * j] = src[16 * j];
+    };
     if constexpr (!QUANT) {
-        float4 *dst = reinterpret_cast<float4 *>(a.P + t * N);
-        for (int i = tid; i < N / 4; i += NT) dst[i] = F4[f4(i)];
+        copy_row(a.P + t * N);
     } else {
-        if (a.rotated) {
-            for (int i = tid; i < N / 4; i += NT)
-                reinterpret_cast<float4 *>(a.rotated + t * N)[i] = F4[f4(i)];
-        }
+        if (a.rotated) copy_row(a.rotated + t * N);
         constexpr int G8 = B / 8;
         constexpr int CHUNKS = N / 8;
         const int64_t orow = a.dest ? a.dest[t] : t;
