@@ -501,7 +501,7 @@ size_t xf_pd_bytes(int64_t T, int S) { return align256(sizeof(double) * XF_K * (
 int launch_proj_tok(const uint16_t *x, int64_t T, int64_t n, int64_t ldx, const float *v, int k, int S,
                     double *pd, float *pf, hipStream_t s, bool f16 = true)
 {
-    ProjTokArgs a{x, ldx, T, n, v, pd, pf, k, S};
+    ProjTokArgs a{x, ldx, T, n, v, pd, pf, k, S, k % 4 == 0 && aligned16(v)};
     const dim3 grid((unsigned)((T + 63) / 64), (unsigned)S);
     if (f16) hipLaunchKernelGGL(proj_tok_kernel<true>, grid, dim3(256), 0, s, a);
     else hipLaunchKernelGGL(proj_tok_kernel<false>, grid, dim3(256), 0, s, a);

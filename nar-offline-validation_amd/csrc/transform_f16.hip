@@ -38,6 +38,7 @@ struct ProjTokArgs {
     double *pd;               // [T][S][XF_K] fp64 chunk sums (S == 1: RN32 of the sum), or null
     float *pf;                // [T][S*k] fp32 chunk sums (each rounded once), or null
     int k, S;                 // chunk = n / S channels, a multiple of 128
+    bool v4;                  // k % 4 == 0 and v 16-byte aligned: V rows by float4 loads
 };
 
 constexpr int PT_TC = 128;                  // channels per LDS tile
@@ -68,10 +69,20 @@ proj_tok_kernel(ProjTokArgs a)
     const float *vsrc = a.v + (c0 + vc) * a.k;
     const int xoff = lr * PT_ROWB + lq * 64, voff = PT_XB + 32 * tid;
     float vf[4];
+    // branch-free: out-of-rank slots load a valid element and are replaced by 0
     auto load_v = [&](int tile) {
+        const float *vt = vsrc + (int64_t)tile * PT_TC * a.k;
+        if (a.v4) {
+            const float4 f = *reinterpret_cast<const float4 *>(vt + (vr < a.k ? vr : 0));
+            const bool ok = vr < a.k;
+            vf[0] = ok ? f.x : 0.0f; vf[1] = ok ? f.y : 0.0f; vf[2] = ok ? f.z : 0.0f; vf[3] = ok ? f.w : 0.0f;
+        } else {
 #pragma unroll
-        for (int j = 0; j < 4; j++)
-            vf[j] = vr + j < a.k ? vsrc[(int64_t)tile * PT_TC * a.k + vr + j] : 0.0f;
+            for (int j = 0; j < 4; j++) {
+                const float f = vt[vr + j < a.k ? vr + j : 0];
+                vf[j] = vr + j < a.k ? f : 0.0f;
+            }
+        }
     };
     auto store_v = [&](uint8_t *buf) {
         double2 *dv = reinterpret_cast<double2 *>(buf + voff);
