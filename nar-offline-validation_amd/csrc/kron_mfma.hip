@@ -56,6 +56,10 @@ kron_mfma_kernel(KronArgs a)
     const int l16 = tid & 15;
     const int row = tid >> 4;
     const int chunk = lane_chunk(l16);
+    float sj[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) sj[j] = ((chunk >> j) & 1) ? -1.0f : 1.0f;
+    const float sigma = sj[0] * sj[1] * sj[2] * sj[3];
 
     // Paley rows as the MFMA A operand, lane l's fragment at hat[mt][l]: built
     // by wave 0 only (the lane-indexed table lookup is a select chain) and read
@@ -90,65 +94,48 @@ kron_mfma_kernel(KronArgs a)
     for (int h = 0; h < NH; h++)
         xw[h] = *reinterpret_cast<const uint4 *>(a.x + t * a.ldx + s * Q + h * 128 + chunk * 8);
     for (; t < a.T; t += gridDim.x) {
-    // ---- phase 1 (identical arithmetic to rq_row_kernel): row `row` transforms segment `row`
+    // ---- phase 1 (the arithmetic of rq_row_kernel): row `row` transforms segment `row`
     {
         float v[NV];
-#pragma unroll
-        for (int h = 0; h < NH; h++) {
-            v[h * 8 + 0] = bf16lo(xw[h].x); v[h * 8 + 1] = bf16hi(xw[h].x);
-            v[h * 8 + 2] = bf16lo(xw[h].y); v[h * 8 + 3] = bf16hi(xw[h].y);
-            v[h * 8 + 4] = bf16lo(xw[h].z); v[h * 8 + 5] = bf16hi(xw[h].z);
-            v[h * 8 + 6] = bf16lo(xw[h].w); v[h * 8 + 7] = bf16hi(xw[h].w);
-        }
+        unpack_x<NH>(v, xw);
         if constexpr (PERSIST) {
             const int64_t tn = t + gridDim.x < a.T ? t + gridDim.x : a.T - 1;
 #pragma unroll
             for (int h = 0; h < NH; h++)
                 xw[h] = *reinterpret_cast<const uint4 *>(a.x + tn * a.ldx + s * Q + h * 128 + chunk * 8);
         }
-        if (a.signs) {
+        if (a.signs) apply_signs<NH>(v, a.signs + s * Q + chunk * 8);
+        fwht_lane_stages<NH>(v);
+        // cross-lane stages as one v_fmac with a DPP source: v + s_j * partner.
+        // The lower lane of each pair holds the sum, the upper lane the negated
+        // difference, so after the four stages the lane holds sigma * (true
+        // value) with sigma = s_0 s_1 s_2 s_3; fma with a +-1 multiplier rounds
+        // exactly like the add or subtract, and RN is odd-symmetric, so every
+        // nonzero value is bit-exact; sigma is folded into the division below.
+        fwht_xlane_signed(v, sj);
+        fwht_h_stages<NH>(v);
+        // Only a zero (or a value below 2^-100, where the division shortcut is
+        // not exact) can differ: a zero's sign follows sigma instead of IEEE
+        // x + (-x) = +0.  A wave holding one recomputes its rows with the plain
+        // butterflies and the IEEE division (x is re-read).
+        float amin = __builtin_fabsf(v[0]);
+#pragma unroll
+        for (int i = 1; i < NV; i++) amin = fminf(amin, __builtin_fabsf(v[i]));
+        if (__builtin_expect(__any(amin < 0x1p-100f), 0)) {
+            uint4 xr[NH];
 #pragma unroll
             for (int h = 0; h < NH; h++)
+                xr[h] = *reinterpret_cast<const uint4 *>(a.x + t * a.ldx + s * Q + h * 128 + chunk * 8);
+            unpack_x<NH>(v, xr);
+            if (a.signs) apply_signs<NH>(v, a.signs + s * Q + chunk * 8);
+            fwht_lane_stages<NH>(v);
+            fwht_xlane_plain(v, sj);
+            fwht_h_stages<NH>(v);
 #pragma unroll
-                for (int e = 0; e < 8; e++) v[h * 8 + e] *= a.signs[s * Q + h * 128 + chunk * 8 + e];
+            for (int i = 0; i < NV; i++) v[i] = v[i] / a.sq;
+        } else {
+            div_sqrt_q_fast<Q>(v, sigma * a.sq, sigma * a.rsq);
         }
-#pragma unroll
-        for (int wd = 1; wd < 8; wd <<= 1)
-#pragma unroll
-            for (int h = 0; h < NH; h++)
-#pragma unroll
-                for (int e = 0; e < 8; e++)
-                    if (!(e & wd)) {
-                        float x0 = v[h * 8 + e], x1 = v[h * 8 + e + wd];
-                        v[h * 8 + e] = x0 + x1;
-                        v[h * 8 + e + wd] = x0 - x1;
-                    }
-        {
-            const float s0 = (chunk & 1) ? -1.0f : 1.0f;
-            const float s1 = (chunk & 2) ? -1.0f : 1.0f;
-            const float s2 = (chunk & 4) ? -1.0f : 1.0f;
-            const float s3 = (chunk & 8) ? -1.0f : 1.0f;
-#pragma unroll
-            for (int i = 0; i < NV; i++) v[i] = __builtin_fmaf(s0, v[i], xchg<0>(v[i]));
-#pragma unroll
-            for (int i = 0; i < NV; i++) v[i] = __builtin_fmaf(s1, v[i], xchg<1>(v[i]));
-#pragma unroll
-            for (int i = 0; i < NV; i++) v[i] = __builtin_fmaf(s2, v[i], xchg<2>(v[i]));
-#pragma unroll
-            for (int i = 0; i < NV; i++) v[i] = __builtin_fmaf(s3, v[i], xchg<3>(v[i]));
-        }
-#pragma unroll
-        for (int wh = 1; wh < NH; wh <<= 1)
-#pragma unroll
-            for (int h = 0; h < NH; h++)
-                if (!(h & wh))
-#pragma unroll
-                    for (int e = 0; e < 8; e++) {
-                        float x0 = v[h * 8 + e], x1 = v[(h + wh) * 8 + e];
-                        v[h * 8 + e] = x0 + x1;
-                        v[(h + wh) * 8 + e] = x0 - x1;
-                    }
-        div_sqrt_q<Q>(v, a.sq, a.rsq);
 #pragma unroll
         for (int h = 0; h < NH; h++) {
             float4 *d = reinterpret_cast<float4 *>(F + s * QS + ((h * 128 + chunk * 8) ^ fsw(s)));

@@ -130,6 +130,131 @@ __device__ __forceinline__ void fwht_row(float (&v)[8 * NH], int chunk)
                 }
 }
 
+// The stages of fwht_row as separate steps, for kernels that interleave other
+// work or take the cross-lane stages in the signed form below.  x arrives as
+// NH uint4 words of 8 bf16 (element h*8 + e at offset h*128 + e of the lane's
+// chunk).
+template <int NH>
+__device__ __forceinline__ void unpack_x(float (&v)[8 * NH], const uint4 (&xw)[NH])
+{
+#pragma unroll
+    for (int h = 0; h < NH; h++) {
+        v[h * 8 + 0] = bf16lo(xw[h].x); v[h * 8 + 1] = bf16hi(xw[h].x);
+        v[h * 8 + 2] = bf16lo(xw[h].y); v[h * 8 + 3] = bf16hi(xw[h].y);
+        v[h * 8 + 4] = bf16lo(xw[h].z); v[h * 8 + 5] = bf16hi(xw[h].z);
+        v[h * 8 + 6] = bf16lo(xw[h].w); v[h * 8 + 7] = bf16hi(xw[h].w);
+    }
+}
+
+// v *= signs (the lane's chunk of the segment starts at sg)
+template <int NH>
+__device__ __forceinline__ void apply_signs(float (&v)[8 * NH], const float *sg)
+{
+#pragma unroll
+    for (int h = 0; h < NH; h++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) v[h * 8 + e] *= sg[h * 128 + e];
+}
+
+// stages of width 1, 2, 4 (within the lane's 8 consecutive positions)
+template <int NH>
+__device__ __forceinline__ void fwht_lane_stages(float (&v)[8 * NH])
+{
+#pragma unroll
+    for (int w = 1; w < 8; w <<= 1)
+#pragma unroll
+        for (int h = 0; h < NH; h++)
+#pragma unroll
+            for (int e = 0; e < 8; e++)
+                if (!(e & w)) {
+                    float x0 = v[h * 8 + e], x1 = v[h * 8 + e + w];
+                    v[h * 8 + e] = x0 + x1;
+                    v[h * 8 + e + w] = x0 - x1;
+                }
+}
+
+// stages of width 8 .. 64 across the 16 lanes of the row, IEEE form: the lower
+// lane of a pair computes own + partner, the upper lane partner - own
+// (sj[j] = -1 on lanes whose chunk bit j is set)
+template <int NV>
+__device__ __forceinline__ void fwht_xlane_plain(float (&v)[NV], const float (&sj)[4])
+{
+#pragma unroll
+    for (int i = 0; i < NV; i++) v[i] = __builtin_fmaf(sj[0], v[i], dpp_f32<DPP_XOR1>(v[i]));
+#pragma unroll
+    for (int i = 0; i < NV; i++) v[i] = __builtin_fmaf(sj[1], v[i], dpp_f32<DPP_XOR2>(v[i]));
+#pragma unroll
+    for (int i = 0; i < NV; i++) v[i] = __builtin_fmaf(sj[2], v[i], dpp_f32<DPP_XOR7>(v[i]));
+#pragma unroll
+    for (int i = 0; i < NV; i++) v[i] = __builtin_fmaf(sj[3], v[i], dpp_f32<DPP_XOR15>(v[i]));
+}
+
+// The same stages as one v_fmac_f32 with a DPP source each: v + sj * partner.
+// Every lane of a pair holds the same sign factor before a stage, so the lower
+// lane gets sign * (a + b) and the upper lane -sign * (b - a): after the four
+// stages v = sigma * (IEEE result), sigma = sj[0] sj[1] sj[2] sj[3], for every
+// nonzero result (fma with a +-1 multiplier is one rounding of the same exact
+// value, and RN is odd-symmetric).  A zero result can carry the wrong sign.
+//
+// Written as v_fmac_f32_dpp directly (the compiler keeps a separate DPP move).
+// A DPP read of a VGPR needs 2 wait states after a VALU write of it: each block
+// of 8 starts with s_nop 1, and within a stage every register is written once
+// and read by DPP only in the next stage, 8 or more instructions later.
+#define NARHIP_FMAC_DPP8(CTRL)                                                              \
+    asm volatile("s_nop 1\n\t"                                                              \
+                 "v_fmac_f32_dpp %0, %0, %8 " CTRL " row_mask:0xf bank_mask:0xf\n\t"        \
+                 "v_fmac_f32_dpp %1, %1, %8 " CTRL " row_mask:0xf bank_mask:0xf\n\t"        \
+                 "v_fmac_f32_dpp %2, %2, %8 " CTRL " row_mask:0xf bank_mask:0xf\n\t"        \
+                 "v_fmac_f32_dpp %3, %3, %8 " CTRL " row_mask:0xf bank_mask:0xf\n\t"        \
+                 "v_fmac_f32_dpp %4, %4, %8 " CTRL " row_mask:0xf bank_mask:0xf\n\t"        \
+                 "v_fmac_f32_dpp %5, %5, %8 " CTRL " row_mask:0xf bank_mask:0xf\n\t"        \
+                 "v_fmac_f32_dpp %6, %6, %8 " CTRL " row_mask:0xf bank_mask:0xf\n\t"        \
+                 "v_fmac_f32_dpp %7, %7, %8 " CTRL " row_mask:0xf bank_mask:0xf"            \
+                 : "+v"(p[0]), "+v"(p[1]), "+v"(p[2]), "+v"(p[3]), "+v"(p[4]), "+v"(p[5]),   \
+                   "+v"(p[6]), "+v"(p[7])                                                    \
+                 : "v"(m))
+
+template <int J>
+__device__ __forceinline__ void fmac_dpp8(float *p, float m)
+{
+    if constexpr (J == 0) NARHIP_FMAC_DPP8("quad_perm:[1,0,3,2]");
+    else if constexpr (J == 1) NARHIP_FMAC_DPP8("quad_perm:[2,3,0,1]");
+    else if constexpr (J == 2) NARHIP_FMAC_DPP8("row_half_mirror");
+    else NARHIP_FMAC_DPP8("row_mirror");
+}
+#undef NARHIP_FMAC_DPP8
+
+template <int NV>
+__device__ __forceinline__ void fwht_xlane_signed(float (&v)[NV], const float (&sj)[4])
+{
+    static_assert(NV % 8 == 0 && NV >= 16, "blocks of 8, two or more per stage");
+#pragma unroll
+    for (int b = 0; b < NV; b += 8) fmac_dpp8<0>(v + b, sj[0]);
+#pragma unroll
+    for (int b = 0; b < NV; b += 8) fmac_dpp8<1>(v + b, sj[1]);
+#pragma unroll
+    for (int b = 0; b < NV; b += 8) fmac_dpp8<2>(v + b, sj[2]);
+#pragma unroll
+    for (int b = 0; b < NV; b += 8) fmac_dpp8<3>(v + b, sj[3]);
+}
+
+// stages of width 128 .. 64 NH (across the lane's NH chunks)
+template <int NH>
+__device__ __forceinline__ void fwht_h_stages(float (&v)[8 * NH])
+{
+#pragma unroll
+    for (int wh = 1; wh < NH; wh <<= 1)
+#pragma unroll
+        for (int h = 0; h < NH; h++)
+            if (!(h & wh))
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    float x0 = v[h * 8 + e], x1 = v[(h + wh) * 8 + e];
+                    v[h * 8 + e] = x0 + x1;
+                    v[(h + wh) * 8 + e] = x0 - x1;
+                }
+}
+
 // Sum over the 16 lanes of a row in fp64; every lane receives the identical value.
 __device__ __forceinline__ double row_sum64(double v)
 {
@@ -246,6 +371,25 @@ __device__ __forceinline__ void div_sqrt_q(float (&v)[NV], float c, float rc)
                 const float r = __builtin_fmaf(q0, c, -v[i]);
                 v[i] = __builtin_fmaf(-r, rc, q0);
             }
+        }
+    }
+}
+
+// RN(v / c) without the range check of div_sqrt_q: every |v| must be >= 2^-100
+// (or Q a power of 4).  c and rc may carry a common sign (c = sigma fp32(sqrt Q),
+// rc = sigma RN(1/fp32(sqrt Q))): then the result is RN((sigma v) / fp32(sqrt Q)).
+template <int Q, int NV>
+__device__ __forceinline__ void div_sqrt_q_fast(float (&v)[NV], float c, float rc)
+{
+    constexpr bool pow4 = (Q & (Q - 1)) == 0 && (Q & 0x55555555) == Q;
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        if constexpr (pow4) {
+            v[i] *= rc;
+        } else {
+            const float q0 = v[i] * rc;
+            const float r = __builtin_fmaf(q0, c, -v[i]);
+            v[i] = __builtin_fmaf(-r, rc, q0);
         }
     }
 }

@@ -160,3 +160,51 @@ def test_projection_mfma_close_to_exact():
     rel = np.abs(u_m - u_ref) / (np.abs(u_ref) + np.sqrt((u_ref ** 2).mean()))
     print(f"  projection max rel err {rel.max():.3e}")
     assert rel.max() < 2.0 ** -20
+
+
+def _zero_producing_rows(n: int, t: int) -> np.ndarray:
+    """Rows whose FWHT outputs contain exact zeros (zero and constant rows, a
+    rounding-boundary ramp, a common offset, an outlier on noise) interleaved
+    with plain noise rows, so that waves with and without a zero both occur."""
+    rng = np.random.default_rng(29)
+    noise = rng.standard_normal((t, n)).astype(np.float32)
+    rows = noise.copy()
+    rows[0] = 0.0
+    rows[2] = 0.5
+    rows[4] = ((np.arange(n) % 15 - 7 + 0.5) / 7).astype(np.float32)
+    rows[6] = 64 + noise[6] * 0.03125
+    rows[8, 0] = 128.0
+    rows[9, : n // 2] = 0.0
+    return O.bf16_bits(rows)
+
+
+@pytest.mark.parametrize("shape", [(12, 256, 3072, 64), (28, 512, 14336, 128), (28, 1024, 28672, 128)])
+def test_kron_mfma_zero_results_keep_ieee_sign(shape):
+    """The Kronecker kernel's cross-lane butterflies run in a sign-folded form
+    that is bit-exact for every nonzero value; a wave holding an exact zero (or a
+    value below 2^-100) recomputes with the plain butterflies.  Rows that make
+    zeros must therefore give the oracle's zero signs in the rotated rows and the
+    oracle's fp16 zero-point bits (fp16(-0) would differ), k = 0 on the MFMA path."""
+    m, q, n, b = shape
+    print(f"[test_kron_mfma_zero_results_keep_ieee_sign] {shape}", flush=True)
+    t = 12
+    bits = _zero_producing_rows(n, t)
+    x = to_dev_bf16(bits)
+    rot = torch.empty((t, n), dtype=torch.float32, device="cuda")
+    codes, scales, zeros = ops.rotate_quant(x, hadamard=(m, q), group=b, rotated=rot)
+    torch.cuda.synchronize()
+    ref_rot = O.rotate(O.bf16_to_f32(bits), m, q)
+    ref = O.quant(ref_rot, b)
+    rot = rot.cpu().numpy()
+    z = ref_rot == 0
+    assert z.any()
+    # where the oracle is zero the kernel gives the same zero, or (MFMA class) a
+    # residual of the split Paley sums far below the tolerance
+    both = z & (rot == 0)
+    assert both.sum() >= 0.99 * z.sum()
+    assert np.array_equal(np.signbit(rot[both]), np.signbit(ref_rot[both]))
+    assert O.rotated_error(rot, ref_rot) <= 2.0 ** -23
+    assert np.array_equal(f16_bits(zeros), ref.zeros)
+    rep = O.compare_quant(ref_rot, ref, O.unpack(codes.cpu().numpy(), n), f16_bits(scales), f16_bits(zeros), b,
+                          rel_err=2.0 ** -23)
+    assert rep.within_contract(), rep
