@@ -375,35 +375,6 @@ int launch_proj_mfma(const uint16_t *x, int64_t T, int64_t n, int64_t ldx, const
 // process.  The full-row rank path runs the projection (and the fold of its
 // partials) on it, concurrently with the Kronecker transform on the caller's
 // stream: the transform is VALU-bound, the projection waits on memory.
-struct SideStream {
-    hipStream_t s = nullptr;
-    hipEvent_t fork = nullptr, join = nullptr;
-};
-
-int side_stream(SideStream *&out)
-{
-    constexpr int MAXDEV = 64;
-    static thread_local SideStream per_dev[MAXDEV];
-    int dev = 0;
-    hipError_t e = hipGetDevice(&dev);
-    if (e != hipSuccess) return fail(NARHIP_EHIP, "hipGetDevice: %s", hipGetErrorString(e));
-    if (dev < 0 || dev >= MAXDEV) return fail(NARHIP_EHIP, "device index %d", dev);
-    SideStream &ss = per_dev[dev];
-    if (!ss.s) {
-        if ((e = hipStreamCreateWithFlags(&ss.s, hipStreamNonBlocking)) != hipSuccess ||
-            (e = hipEventCreateWithFlags(&ss.fork, hipEventDisableTiming)) != hipSuccess ||
-            (e = hipEventCreateWithFlags(&ss.join, hipEventDisableTiming)) != hipSuccess)
-            return fail(NARHIP_EHIP, "side stream: %s", hipGetErrorString(e));
-    }
-    out = &ss;
-    return NARHIP_OK;
-}
-
-int hip_ok(hipError_t e, const char *what)
-{
-    return e == hipSuccess ? NARHIP_OK : fail(NARHIP_EHIP, "%s: %s", what, hipGetErrorString(e));
-}
-
 int launch_fold_u(const float *partial, int splits, int k, int kp, int64_t T, __bf16 *u3, hipStream_t s)
 {
     const int64_t n = T * kp;
@@ -665,21 +636,12 @@ int run_rotate_quant(const void *x_bf16, int64_t T, int64_t n, int64_t ldx, int 
             const int64_t tn = T - t0 < p.chunk ? T - t0 : p.chunk;
             const uint16_t *xc = x + t0 * ldx;
             const float *part = partial ? partial + t0 * (int64_t)splits * k : nullptr;
-            // projection and fold on the side stream (forked from s after all
-            // earlier work on s, joined back before the correction)
-            SideStream *ss = nullptr;
-            constexpr int64_t CONCURRENT_MIN = int64_t(1) << 25;   // elements: below, fork/join latency dominates
-            if (p.need_proj && tn * n < CONCURRENT_MIN) {
+            // projection and fold first, on the caller's stream: x then sits in
+            // the Infinity Cache for the transform (measured faster than running
+            // them on a second stream under the transform)
+            if (p.need_proj) {
                 if ((rc = launch_proj_mfma(xc, tn, n, ldx, prep, k, p.splits, proj, s))) return rc;
                 if ((rc = launch_fold_u(proj, p.splits, k, kp32(k), tn, u3, s))) return rc;
-            } else if (p.need_proj) {
-                if ((rc = side_stream(ss))) return rc;
-                if ((rc = hip_ok(hipEventRecord(ss->fork, s), "hipEventRecord")) ||
-                    (rc = hip_ok(hipStreamWaitEvent(ss->s, ss->fork, 0), "hipStreamWaitEvent")))
-                    return rc;
-                if ((rc = launch_proj_mfma(xc, tn, n, ldx, prep, k, p.splits, proj, ss->s))) return rc;
-                if ((rc = launch_fold_u(proj, p.splits, k, kp32(k), tn, u3, ss->s))) return rc;
-                if ((rc = hip_ok(hipEventRecord(ss->join, ss->s), "hipEventRecord"))) return rc;
             } else {
                 if ((rc = launch_fold_u(part, splits, k, kp32(k), tn, u3, s))) return rc;
             }
@@ -694,7 +656,6 @@ int run_rotate_quant(const void *x_bf16, int64_t T, int64_t n, int64_t ldx, int 
                 sa.codes = nullptr; sa.rotated = Pbuf; sa.sq = f32_sqrt(q); sa.rsq = 1.0f / sa.sq;
                 if ((rc = launch_seg(sa, q, group, RANK_NONE, s))) return rc;
             }
-            if (ss && (rc = hip_ok(hipStreamWaitEvent(s, ss->join, 0), "hipStreamWaitEvent"))) return rc;
             CorrQuantArgs ca{};
             ca.P = Pbuf; ca.T = tn; ca.n = n; ca.u3 = u3;
             ca.dummy = reinterpret_cast<uint8_t *>(u3) + align256(u3_bytes(tn, k));
