@@ -46,7 +46,7 @@ MFMA_UTIL = {
     "downproj_70b": {"proj_mfma": 0.271, "corr_quant": 0.287},
 }
 TRAFFIC_BYTES = {
-    "downproj_8b": 1572.4e6,
+    "downproj_8b": 1570.5e6,
     "downproj_70b": 6283.5e6,
     "qproj_3b": 171.5e6,
     "kcache_3b": 5.8e6,
@@ -203,7 +203,7 @@ def main() -> int:
     ms_step = ms_total / args.steps
 
     # Roofline of the operator call.  One call is one dispatch sequence on the
-    # current stream (full-row rank: proj_mfma -> kron_mfma / rq_seg -> fold_u
+    # current stream (full-row rank: proj_mfma -> fold_u -> kron_mfma / rq_seg
     # -> corr_quant; otherwise one rq_seg / kron dispatch), so the per-launch
     # duration is ms_step, HIP-event timed above on that stream.  Algorithmic
     # bytes: T*(2n + n/2 + 4n/b) + factor bytes.  Traffic: HBM bytes per call
@@ -213,7 +213,7 @@ def main() -> int:
     achieved = alg_bytes / (ms_step * 1e-3) / 1e9
     kron = w.hadamard[0] > 1
     if full_row_rank and mode != ops.RANK_EXACT and (w.k >= 16 or mode == ops.RANK_MFMA):
-        kernels = f"proj_mfma + {'kron_mfma' if kron else 'rq_seg'} + fold_u + corr_quant"
+        kernels = f"proj_mfma + fold_u + {'kron_mfma' if kron else 'rq_seg'} + corr_quant"
     elif full_row_rank and mode == ops.RANK_AUTO and not kron:
         kernels = "proj_f64 + fold_f64 + rq_seg"
     elif full_row_rank:
