@@ -61,8 +61,10 @@ struct ProjMfmaArgs {
 // grid (ceil(T/128), splits), block 256.  Wave w owns tokens 32w..32w+31 of
 // the 128-token tile as two 16-token N tiles; all MT rank tiles of 16 rows.
 // The split's channels are walked in blocks of 64: the V terms of a block are
-// staged in LDS (two buffers, one barrier per block) and x of the next block is
-// requested while the current block's MFMAs run.
+// staged in LDS (two buffers, one barrier per block); x runs three blocks
+// ahead in a register ring and V two blocks ahead (down_proj 70B, 16384 x
+// 28672, k = 64: 315 -> 258 us; one block ahead of both left a single block of
+// x in flight per wave).
 template <int MT>
 __global__ void __launch_bounds__(256, 2)
 proj_mfma_kernel(ProjMfmaArgs a)
@@ -73,6 +75,9 @@ proj_mfma_kernel(ProjMfmaArgs a)
     constexpr int VSTR = KB + 8;            // padded LDS row (bf16)
     constexpr int VPIECES = 3 * ROWS * (KB / 8);              // 16-byte pieces per block
     constexpr int VPT = (VPIECES + 255) / 256;                // pieces per thread
+    constexpr bool VFULL = VPIECES % 256 == 0;                // no guard: loads outside branches
+    constexpr int XD = 3;                   // x blocks in flight per wave (12 KB; at 512 workgroups
+                                            // two waves per SIMD must cover HBM latency)
     __shared__ __align__(16) __bf16 vs[2][3][ROWS][VSTR];
     const int tid = threadIdx.x;
     const int lane = tid & 63, w = tid >> 6;
@@ -104,68 +109,70 @@ proj_mfma_kernel(ProjMfmaArgs a)
 #pragma unroll
         for (int nt = 0; nt < 2; nt++) { acc_h[mt][nt] = zero4(); acc_l[mt][nt] = zero4(); }
 
-    // prologue: block 0
-    bf16x8 xa[KB / 32][2];
-    {
-        bf16x8 vt[VPT];
+    // Loads run ahead of use: x of block b + XD is requested after block b's
+    // MFMAs (slot b % XD of a register ring), V of block b + 2 before them
+    // (slot b % 2); V of block b + 1, requested one block earlier, goes to LDS
+    // at the end of block b.  Memory operations complete in order, so waiting
+    // for that V load waits only for the x of block b + 1 as well.  The loop is
+    // unrolled by 2 XD so every slot is a fixed register range.  Requests past
+    // the split's last block re-request that block (L2 hits).
+    bf16x8 xq[XD][KB / 32][2], vr[2][VPT];
+    auto load_v = [&](bf16x8 (&dst)[VPT], int blk) {
 #pragma unroll
         for (int i = 0; i < VPT; i++) {
             const int p = tid + 256 * i;
-            if (p < VPIECES) vt[i] = load_bf16x8(v_src(p, 0));
+            if (VFULL || p < VPIECES) dst[i] = load_bf16x8(v_src(p, blk));
         }
-#pragma unroll
-        for (int ks = 0; ks < KB / 32; ks++)
-#pragma unroll
-            for (int nt = 0; nt < 2; nt++) xa[ks][nt] = *reinterpret_cast<const bf16x8 *>(xrow[nt] + 32 * ks);
+    };
+    auto store_v = [&](const bf16x8 (&src)[VPT], int buf) {
 #pragma unroll
         for (int i = 0; i < VPT; i++) {
             const int p = tid + 256 * i;
-            if (p < VPIECES) *reinterpret_cast<bf16x8 *>(v_dst(p, 0)) = vt[i];
+            if (VFULL || p < VPIECES) *reinterpret_cast<bf16x8 *>(v_dst(p, buf)) = src[i];
         }
-        __syncthreads();
-    }
-    for (int b = 0; b < nblk; b++) {
-        // next block (the last iteration re-requests its own block: L2 hits)
-        const int bn = b + 1 < nblk ? b + 1 : b;
-        bf16x8 vt[VPT], xn[KB / 32][2];
-#pragma unroll
-        for (int i = 0; i < VPT; i++) {
-            const int p = tid + 256 * i;
-            if (p < VPIECES) vt[i] = load_bf16x8(v_src(p, bn));
-        }
+    };
+    auto load_x = [&](bf16x8 (&dst)[KB / 32][2], int blk) {
+        const int64_t bo = (int64_t)(blk < nblk ? blk : nblk - 1) * KB;
 #pragma unroll
         for (int ks = 0; ks < KB / 32; ks++)
 #pragma unroll
             for (int nt = 0; nt < 2; nt++)
-                xn[ks][nt] = *reinterpret_cast<const bf16x8 *>(xrow[nt] + (int64_t)bn * KB + 32 * ks);
-        __builtin_amdgcn_sched_barrier(0);
-        const int cur = b & 1;
+                dst[ks][nt] = *reinterpret_cast<const bf16x8 *>(xrow[nt] + bo + 32 * ks);
+    };
+    load_v(vr[0], 0);
 #pragma unroll
-        for (int ks = 0; ks < KB / 32; ks++) {
+    for (int d = 0; d < XD; d++) load_x(xq[d], d);
+    load_v(vr[1], nblk > 1 ? 1 : 0);
+    store_v(vr[0], 0);
+    __syncthreads();
+    for (int b0 = 0; b0 < nblk; b0 += 2 * XD) {
 #pragma unroll
-            for (int mt = 0; mt < MT; mt++) {
-                const bf16x8 ah = *reinterpret_cast<const bf16x8 *>(&vs[cur][0][16 * mt + c16][32 * ks + 8 * g]);
-                const bf16x8 am = *reinterpret_cast<const bf16x8 *>(&vs[cur][1][16 * mt + c16][32 * ks + 8 * g]);
-                const bf16x8 al = *reinterpret_cast<const bf16x8 *>(&vs[cur][2][16 * mt + c16][32 * ks + 8 * g]);
+        for (int d = 0; d < 2 * XD; d++) {
+            const int b = b0 + d;
+            if (b >= nblk) break;
+            load_v(vr[d % 2], b + 2 < nblk ? b + 2 : nblk - 1);
+            __builtin_amdgcn_sched_barrier(0);
+            const int cur = b & 1;
 #pragma unroll
-                for (int nt = 0; nt < 2; nt++) {
-                    acc_h[mt][nt] = mfma_bf16(ah, xa[ks][nt], acc_h[mt][nt]);
-                    acc_l[mt][nt] = mfma_bf16(am, xa[ks][nt], acc_l[mt][nt]);
-                    acc_l[mt][nt] = mfma_bf16(al, xa[ks][nt], acc_l[mt][nt]);
+            for (int ks = 0; ks < KB / 32; ks++) {
+#pragma unroll
+                for (int mt = 0; mt < MT; mt++) {
+                    const bf16x8 ah = *reinterpret_cast<const bf16x8 *>(&vs[cur][0][16 * mt + c16][32 * ks + 8 * g]);
+                    const bf16x8 am = *reinterpret_cast<const bf16x8 *>(&vs[cur][1][16 * mt + c16][32 * ks + 8 * g]);
+                    const bf16x8 al = *reinterpret_cast<const bf16x8 *>(&vs[cur][2][16 * mt + c16][32 * ks + 8 * g]);
+#pragma unroll
+                    for (int nt = 0; nt < 2; nt++) {
+                        acc_h[mt][nt] = mfma_bf16(ah, xq[d % XD][ks][nt], acc_h[mt][nt]);
+                        acc_l[mt][nt] = mfma_bf16(am, xq[d % XD][ks][nt], acc_l[mt][nt]);
+                        acc_l[mt][nt] = mfma_bf16(al, xq[d % XD][ks][nt], acc_l[mt][nt]);
+                    }
                 }
             }
+            __builtin_amdgcn_sched_barrier(0);
+            load_x(xq[d % XD], b + XD);
+            store_v(vr[(d + 1) % 2], cur ^ 1);
+            __syncthreads();
         }
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int i = 0; i < VPT; i++) {
-            const int p = tid + 256 * i;
-            if (p < VPIECES) *reinterpret_cast<bf16x8 *>(v_dst(p, cur ^ 1)) = vt[i];
-        }
-        __syncthreads();
-#pragma unroll
-        for (int ks = 0; ks < KB / 32; ks++)
-#pragma unroll
-            for (int nt = 0; nt < 2; nt++) xa[ks][nt] = xn[ks][nt];
     }
 #pragma unroll
     for (int nt = 0; nt < 2; nt++) {
