@@ -114,14 +114,14 @@ kron_mfma_kernel(KronArgs a)
         // nonzero value is bit-exact; sigma is folded into the division below.
         fwht_xlane_signed(v, sj);
         fwht_h_stages<NH>(v);
-        // Only a zero (or a value below 2^-100, where the division shortcut is
-        // not exact) can differ: a zero's sign follows sigma instead of IEEE
+        // Only a zero (or a value below div_sqrt_q_min, where the division
+        // shortcut is not exact) can differ: a zero's sign follows sigma instead of IEEE
         // x + (-x) = +0.  A wave holding one recomputes its rows with the plain
         // butterflies and the IEEE division (x is re-read).
         float amin = __builtin_fabsf(v[0]);
 #pragma unroll
         for (int i = 1; i < NV; i++) amin = fminf(amin, __builtin_fabsf(v[i]));
-        if (__builtin_expect(__any(amin < 0x1p-100f), 0)) {
+        if (__builtin_expect(__any(amin < div_sqrt_q_min<Q>()), 0)) {
             uint4 xr[NH];
 #pragma unroll
             for (int h = 0; h < NH; h++)

@@ -345,11 +345,28 @@ __device__ __forceinline__ uint32_t quant_word8(const float *v, const GroupParam
 //
 // v[i] <- RN(v[i] / c) with c = fp32(sqrt(Q)), rc = RN(1/c).
 // Q a power of 4: c is a power of two and RN(v * rc) is the quotient.
-// Otherwise q0 = v*rc, r = fma(q0, c, -v), q1 = fma(-r, rc, q0), which was
-// checked against the correctly rounded fp32 quotient for every finite fp32 v
-// of both signs and Q in {2, 8, 12, 28, 32, 128, 512, 2048}: equal for all
-// |v| >= 2^-100.  A wave holding any |v| < 2^-100 (zeros included) takes the
-// division instead.
+// Q = 128 and 512: RN(v / c) = fma(v, H, RN(v * L)) with 1/c split as H =
+// RN(1/c), L = RN(1/c - H) (multiplication by a constant in two pieces,
+// Brisebarre and Muller, "Correctly rounded multiplication by arbitrary
+// precision constants", IEEE Trans. Computers 57(2), 2008), checked against
+// the correctly rounded fp32 quotient for every finite fp32 v of both signs:
+// equal for all |v| >= 2^-90 (below, v * L is subnormal).  Two operations.
+// Otherwise q0 = v*rc, r = fma(q0, c, -v), q1 = fma(-r, rc, q0), checked the
+// same way for Q in {2, 8, 12, 28, 32, 128, 512, 2048}: equal for all
+// |v| >= 2^-100.  A wave holding any |v| below the bound (zeros included)
+// takes the division instead.
+template <int Q> struct RecipSqrtQ { static constexpr bool split = false; static constexpr float hi = 0, lo = 0; };
+template <> struct RecipSqrtQ<128> {
+    static constexpr bool split = true;
+    static constexpr float hi = 0x1.6a09e6p-4f, lo = 0x1.9fcef4p-29f;
+};
+template <> struct RecipSqrtQ<512> {
+    static constexpr bool split = true;
+    static constexpr float hi = 0x1.6a09e6p-5f, lo = 0x1.9fcef4p-30f;
+};
+// smallest |v| for which the shortcut of div_sqrt_q_fast<Q> is exact
+template <int Q> constexpr float div_sqrt_q_min() { return RecipSqrtQ<Q>::split ? 0x1p-90f : 0x1p-100f; }
+
 template <int Q, int NV>
 __device__ __forceinline__ void div_sqrt_q(float (&v)[NV], float c, float rc)
 {
@@ -360,10 +377,13 @@ __device__ __forceinline__ void div_sqrt_q(float (&v)[NV], float c, float rc)
     } else {
         bool tiny = false;
 #pragma unroll
-        for (int i = 0; i < NV; i++) tiny |= __builtin_fabsf(v[i]) < 0x1p-100f;
+        for (int i = 0; i < NV; i++) tiny |= __builtin_fabsf(v[i]) < div_sqrt_q_min<Q>();
         if (__builtin_expect(__any(tiny), 0)) {
 #pragma unroll
             for (int i = 0; i < NV; i++) v[i] = v[i] / c;
+        } else if constexpr (RecipSqrtQ<Q>::split) {
+#pragma unroll
+            for (int i = 0; i < NV; i++) v[i] = __builtin_fmaf(v[i], RecipSqrtQ<Q>::hi, v[i] * RecipSqrtQ<Q>::lo);
         } else {
 #pragma unroll
             for (int i = 0; i < NV; i++) {
@@ -375,18 +395,26 @@ __device__ __forceinline__ void div_sqrt_q(float (&v)[NV], float c, float rc)
     }
 }
 
-// RN(v / c) without the range check of div_sqrt_q: every |v| must be >= 2^-100
-// (or Q a power of 4).  c and rc may carry a common sign (c = sigma fp32(sqrt Q),
-// rc = sigma RN(1/fp32(sqrt Q))): then the result is RN((sigma v) / fp32(sqrt Q)).
+// RN(v / c) without the range check of div_sqrt_q: every |v| must be >=
+// div_sqrt_q_min<Q>() (or Q a power of 4).  c and rc may carry a common sign
+// (c = sigma fp32(sqrt Q), rc = sigma RN(1/fp32(sqrt Q))): then the result is
+// RN((sigma v) / fp32(sqrt Q)) (RN is odd-symmetric, so the split constants
+// take the sign of rc).
 template <int Q, int NV>
 __device__ __forceinline__ void div_sqrt_q_fast(float (&v)[NV], float c, float rc)
 {
     constexpr bool pow4 = (Q & (Q - 1)) == 0 && (Q & 0x55555555) == Q;
+    if constexpr (pow4) {
 #pragma unroll
-    for (int i = 0; i < NV; i++) {
-        if constexpr (pow4) {
-            v[i] *= rc;
-        } else {
+        for (int i = 0; i < NV; i++) v[i] *= rc;
+    } else if constexpr (RecipSqrtQ<Q>::split) {
+        const float hi = __builtin_copysignf(RecipSqrtQ<Q>::hi, rc);
+        const float lo = __builtin_copysignf(RecipSqrtQ<Q>::lo, rc);
+#pragma unroll
+        for (int i = 0; i < NV; i++) v[i] = __builtin_fmaf(v[i], hi, v[i] * lo);
+    } else {
+#pragma unroll
+        for (int i = 0; i < NV; i++) {
             const float q0 = v[i] * rc;
             const float r = __builtin_fmaf(q0, c, -v[i]);
             v[i] = __builtin_fmaf(-r, rc, q0);

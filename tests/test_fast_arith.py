@@ -2,9 +2,11 @@
 
 * FWHT normalisation: RN(v / fp32(sqrt(Q))) through a reciprocal and two fma
   corrections, with the IEEE division for |v| < 2^-100
-  (csrc/narhip_device.hpp, div_sqrt_q).  tests/native/div_sqrt_check.c runs
-  the same fp32 operations; this test scans a strided subset of all 2^32 bit
-  patterns (NARHIP_FULL_DIV_SCAN=1 scans all of them).
+  (csrc/narhip_device.hpp, div_sqrt_q); for Q = 128 and 512 as
+  fma(v, HI, v * LO) with 1/c split in two fp32 pieces, with the division for
+  |v| < 2^-90.  tests/native/div_sqrt_check.c runs the same fp32 operations;
+  this test scans a strided subset of all 2^32 bit patterns
+  (NARHIP_FULL_DIV_SCAN=1 scans all of them).
 * Quantizer: rint((x - z) * RN(1/s)) with the exact division only for lanes
   within 2^-18 of a half-integer (quant_code_fast).  Checked against
   rint(RN((x - z) / s)) on random groups and on constructed near-ties.
@@ -38,6 +40,49 @@ def test_div_sqrt_matches_ieee_division():
     for q, bad, checked in rows:
         assert checked > 1_000_000
         assert bad == 0, f"Q={q}: {bad} mismatches"
+
+
+def _split_constants():
+    """(Q, HI, LO) of RecipSqrtQ in the device header, as C float literals."""
+    text = (HERE.parent / "nar-offline-validation_amd" / "csrc" / "narhip_device.hpp").read_text()
+    import re
+    found = re.findall(r"struct RecipSqrtQ<(\d+)> \{[^}]*?hi = ([0-9a-fx.p+-]+)f, lo = ([0-9a-fx.p+-]+)f;", text)
+    return [(int(q), hi, lo) for q, hi, lo in found]
+
+
+def test_split_constants_are_the_reciprocal_split():
+    consts = _split_constants()
+    assert sorted(q for q, _, _ in consts) == [128, 512]
+    for q, hi, lo in consts:
+        c = np.float32(np.sqrt(np.float64(q)))
+        r = 1.0 / np.float64(c)
+        want_hi = np.float32(r)
+        want_lo = np.float32(r - np.float64(want_hi))
+        assert np.float32(float.fromhex(hi)) == want_hi, q
+        assert np.float32(float.fromhex(lo)) == want_lo, q
+
+
+@pytest.mark.skipif(shutil.which("gcc") is None, reason="gcc not available")
+def test_split_division_matches_ieee_division():
+    full = os.environ.get("NARHIP_FULL_DIV_SCAN") == "1"
+    with tempfile.TemporaryDirectory() as tmp:
+        exe = Path(tmp) / "div_sqrt_check"
+        subprocess.run(["gcc", "-O2", "-ffp-contract=off", "-frounding-math", "-o", str(exe),
+                        str(HERE / "native" / "div_sqrt_check.c"), "-lm"], check=True)
+        stride, phase = (1, 0) if full else (4099, 17)
+
+        def scan(q, hi, lo):
+            out = subprocess.run([str(exe), "split", str(stride), str(phase), str(q), hi, lo],
+                                 check=True, capture_output=True, text=True).stdout.split()
+            return int(out[1]), int(out[2])
+
+        for q, hi, lo in _split_constants():
+            bad, checked = scan(q, hi, lo)
+            assert checked > 1_000_000
+            assert bad == 0, f"Q={q}: {bad} mismatches"
+            # a dropped low piece (plain multiplication by RN(1/c)) is caught
+            bad0, _ = scan(q, hi, "0")
+            assert bad0 > 0, q
 
 
 def _exact_codes(x, z, s):
