@@ -144,8 +144,8 @@ def cpu_baseline(w, target_s: float) -> dict:
 def main() -> int:
     args = parse()
     if args.gpus != 1:
-        print("bench.py measures one GPU: every box here has a single MI355X and the path "
-              "shards by tokens with no communication (see DESIGN.md); run with --gpus 1.",
+        print("bench.py measures one GPU: the path is row-independent and shards by tokens "
+              "with no communication beyond a broadcast of the factors; run with --gpus 1.",
               file=sys.stderr)
         return 2
 

@@ -1,8 +1,8 @@
 /*
  * CPU oracle for the NAR online rotate-and-quantize path.
  *
- * TEST INFRASTRUCTURE ONLY.  This file is the checker that the HIP kernels are
- * compared against; it is never linked into, loaded by or called from the
+ * TEST INFRASTRUCTURE ONLY.  This file is the restatement that the HIP kernels
+ * are compared against; it is never linked into, loaded by or called from the
  * product library.  Only tests/, __graft_entry__.smoke() and bench.py's
  * cpu_baseline leg may use it.
  *

@@ -1,6 +1,6 @@
 """Python face of the CPU oracle for the NAR rotate-and-quantize path.
 
-TEST INFRASTRUCTURE ONLY: the checker for the HIP kernels.  Only tests/,
+TEST INFRASTRUCTURE ONLY: the restatement the HIP kernels are tested against.  Only tests/,
 __graft_entry__.smoke() and bench.py's cpu_baseline leg import this module;
 the product package (nar-offline-validation_amd/) never does.
 
