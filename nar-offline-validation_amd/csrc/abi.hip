@@ -121,10 +121,12 @@ PaleyTable paley_table(int m)
 
 float f32_sqrt(int v) { return (float)std::sqrt((double)v); }
 
+// Raise a kernel's dynamic LDS limit for blocks of 48 KB and more (the kernels
+// also hold a few KB of static LDS on top of the dynamic block).
 template <typename K>
 int set_lds(K kernel, size_t lds)
 {
-    if (lds <= 64 * 1024) return NARHIP_OK;
+    if (lds < 48 * 1024) return NARHIP_OK;
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return fail(NARHIP_EHIP, "hipFuncSetAttribute: %s", hipGetErrorString(e));
@@ -208,7 +210,7 @@ int64_t persistent_grid(K kernel, int threads, size_t lds, int64_t work)
 template <int M, int Q, int B>
 int launch_kron_mqb(const KronArgs &a, bool quant, hipStream_t s)
 {
-    const size_t lds = sizeof(float) * M * (Q + KPAD);
+    const size_t lds = sizeof(float) * kron_rows<M>() * (Q + KPAD);
     constexpr bool persist = Q >= 1024;   // 115 KB of LDS: one workgroup per CU
     if (quant) {
         auto k = &kron_mfma_kernel<M, Q, B, true, persist>;

@@ -37,6 +37,12 @@ struct KronArgs {
 constexpr int KPAD = 0;
 __device__ __forceinline__ int fsw(int a) { return (((a >> 3) ^ (a >> 2)) & 1) << 4; }
 
+// Rows of F in LDS.  For M > 16 the block is padded to the MFMA's 32 rows:
+// rows M..31 are zeroed once per workgroup, and phase 2 then reads and writes
+// all 32 rows without row guards (the Paley operand's rows and columns >= M are
+// zero, so the padded rows are rewritten with +0).
+template <int M> constexpr int kron_rows() { return M > 16 ? 32 : M; }
+
 // PERSIST: a grid of at most one wave of workgroups walks all tokens,
 // prefetching the next token's x (pays where LDS allows one workgroup per CU);
 // otherwise one workgroup per token.
@@ -82,6 +88,12 @@ kron_mfma_kernel(KronArgs a)
             }
             hat[mt][lane] = h;
         }
+    }
+
+    constexpr bool PAD = kron_rows<M>() > M;
+    if constexpr (PAD) {
+        for (int i = tid; i < (kron_rows<M>() - M) * (Q / 4); i += NT)
+            reinterpret_cast<float4 *>(F + M * QS)[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
 
     // Persistent over tokens t = blockIdx.x, + gridDim.x, ...; the next token's
@@ -158,7 +170,7 @@ kron_mfma_kernel(KronArgs a)
 #pragma unroll
             for (int j = 0; j < 8; j++) {
                 const int ar = 8 * g + j;
-                f[j] = ar < M ? F[ar * QS + (c ^ fsw(ar))] : 0.0f;
+                f[j] = (PAD || ar < M) ? F[ar * QS + (c ^ fsw(ar))] : 0.0f;
             }
             bf16x8 bh, bm, bl;
             split3x8_trunc(f, bh, bm, bl);
@@ -170,7 +182,7 @@ kron_mfma_kernel(KronArgs a)
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     const int ar = 16 * mt + 4 * g + i;
-                    if (ar < M) F[ar * QS + (c ^ fsw(ar))] = __builtin_fmaf(hm, s1[i], hm * s2[i]);
+                    if (PAD || ar < M) F[ar * QS + (c ^ fsw(ar))] = __builtin_fmaf(hm, s1[i], hm * s2[i]);
                 }
             }
         }
