@@ -39,8 +39,8 @@ __device__ __forceinline__ int fsw(int a) { return (((a >> 3) ^ (a >> 2)) & 1) <
 
 // Rows of F in LDS.  For M > 16 the block is padded to the MFMA's 32 rows:
 // rows M..31 are zeroed once per workgroup, and phase 2 then reads and writes
-// all 32 rows without row guards (the Paley operand's rows and columns >= M are
-// zero, so the padded rows are rewritten with +0).
+// all 32 rows without row guards (the Paley operand's columns >= M are zero,
+// and the padded rows are always rewritten with +0).
 template <int M> constexpr int kron_rows() { return M > 16 ? 32 : M; }
 
 // PERSIST: a grid of at most one wave of workgroups walks all tokens,
@@ -182,7 +182,12 @@ kron_mfma_kernel(KronArgs a)
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     const int ar = 16 * mt + 4 * g + i;
-                    if (PAD || ar < M) F[ar * QS + (c ^ fsw(ar))] = __builtin_fmaf(hm, s1[i], hm * s2[i]);
+                    // padded rows get an exact +0, whatever the column held: an
+                    // Inf or NaN of this token must not reach the next token's
+                    // Paley stage through 0 * NaN
+                    const float p = __builtin_fmaf(hm, s1[i], hm * s2[i]);
+                    if (PAD) F[ar * QS + (c ^ fsw(ar))] = ar < M ? p : 0.0f;
+                    else if (ar < M) F[ar * QS + (c ^ fsw(ar))] = p;
                 }
             }
         }

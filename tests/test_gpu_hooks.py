@@ -91,6 +91,24 @@ def test_full_hadamard_rows_vs_oracle(idx):
         assert O.rotated_error(obs, ref) <= 2.0 ** -21
 
 
+def test_full_hadamard_rows_inf_row_stays_in_its_row():
+    """H28 x H1024 runs on the persistent Kronecker kernel (one workgroup per
+    CU walks several tokens): an Inf in token 0 must not reach token 0 +
+    grid through the zero-padded Paley rows in LDS."""
+    print("[test_full_hadamard_rows_inf_row_stays_in_its_row] 600 x 28672", flush=True)
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal((600, 28 * 1024)).astype(np.float32)
+    xb = torch.from_numpy(x).bfloat16()
+    xb[0, 5] = float("inf")
+    out = hooks.full_hadamard_rows(xb.float().cuda(), None)
+    torch.cuda.synchronize()
+    obs = out.cpu().numpy()
+    ref = O.rotate(xb[1:].float().numpy(), 28, 1024)
+    assert np.isfinite(obs[1:]).all()
+    assert O.rotated_error(obs[1:], ref) <= 2.0 ** -21
+    assert not np.isfinite(obs[0]).all()
+
+
 def test_full_hadamard_rows_rejects_non_bf16_values():
     x = torch.full((2, 128), 1.0 + 2.0 ** -12, device="cuda")
     with pytest.raises(ValueError, match="bf16"):
