@@ -164,14 +164,12 @@ kron_mfma_kernel(KronArgs a)
         for (int mt = 0; mt < NMT; mt++) ha[mt] = hat[mt][lane];
         const float hm = a.hm;
         constexpr int CB = Q / 16;
-        for (int cb = wv; cb < CB; cb += NW) {
-            const int c = 16 * cb + c16;
+        // one 16-column block: ridx(j) is the LDS index of row 8g + j of the
+        // lane's column, widx(mt, i) that of row 16 mt + 4g + i
+        auto paley_block = [&](auto ridx, auto widx) {
             float f[8];
 #pragma unroll
-            for (int j = 0; j < 8; j++) {
-                const int ar = 8 * g + j;
-                f[j] = (PAD || ar < M) ? F[ar * QS + (c ^ fsw(ar))] : 0.0f;
-            }
+            for (int j = 0; j < 8; j++) f[j] = (PAD || 8 * g + j < M) ? F[ridx(j)] : 0.0f;
             bf16x8 bh, bm, bl;
             split3x8_trunc(f, bh, bm, bl);
 #pragma unroll
@@ -186,9 +184,44 @@ kron_mfma_kernel(KronArgs a)
                     // Inf or NaN of this token must not reach the next token's
                     // Paley stage through 0 * NaN
                     const float p = __builtin_fmaf(hm, s1[i], hm * s2[i]);
-                    if (PAD) F[ar * QS + (c ^ fsw(ar))] = ar < M ? p : 0.0f;
-                    else if (ar < M) F[ar * QS + (c ^ fsw(ar))] = p;
+                    if (PAD) F[widx(mt, i)] = ar < M ? p : 0.0f;
+                    else if (ar < M) F[widx(mt, i)] = p;
                 }
+            }
+        };
+        if constexpr (PAD) {
+            // Column block cb of row r sits at r * QS + 16 (cb ^ (fsw(r) >> 4)) + c16.
+            // The flip (fsw(r) >> 4) is (g ^ (j >> 2)) & 1 for the rows 8g + j
+            // read and ((g >> 1) ^ g) & 1 for the rows 16 mt + 4g + i written, and
+            // cb ^ f = cb + dlt(cb & 1, f) with dlt = 16 ((q ^ f) - q).  cb = wv +
+            // NW it alternates parity with it, so per lane and parity of it the
+            // offsets are fixed and every access is a base plus an immediate
+            // (C3: 80 -> 69 VALU instructions per block and wave).  Unrolled only
+            // for the padded blocks: at M = 12 the row guards made it slower.
+            constexpr int ITER = (CB + NW - 1) / NW;
+            static_assert(NW % 2 == 1, "block parity alternates with the iteration");
+            auto dlt = [](int q, int f) { return 16 * ((q ^ f) - q); };
+            const int wq = wv & 1;
+            const int fr0 = g & 1, fr1 = fr0 ^ 1, fw = ((g >> 1) ^ g) & 1;
+            const int rb = 8 * g * QS + 16 * wv + c16, wb = 4 * g * QS + 16 * wv + c16;
+            const int rd0[2] = {rb + dlt(wq, fr0), rb + dlt(wq ^ 1, fr0)};   // rows 8g + 0..3
+            const int rd1[2] = {rb + dlt(wq, fr1), rb + dlt(wq ^ 1, fr1)};   // rows 8g + 4..7
+            const int wr[2] = {wb + dlt(wq, fw), wb + dlt(wq ^ 1, fw)};
+#pragma unroll
+            for (int it = 0; it < ITER; it++) {
+                if (wv + NW * it >= CB) break;
+                const int co = 16 * NW * it;
+                paley_block([&](int j) { return (j < 4 ? rd0[it & 1] : rd1[it & 1]) + j * QS + co; },
+                            [&](int mt, int i) { return wr[it & 1] + (16 * mt + i) * QS + co; });
+            }
+        } else {
+            for (int cb = wv; cb < CB; cb += NW) {
+                const int c = 16 * cb + c16;
+                paley_block([&](int j) { return (8 * g + j) * QS + (c ^ fsw(8 * g + j)); },
+                            [&](int mt, int i) {
+                                const int ar = 16 * mt + 4 * g + i;
+                                return ar * QS + (c ^ fsw(ar));
+                            });
             }
         }
     }
