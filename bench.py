@@ -42,8 +42,8 @@ TRAFFIC_SOURCE = "profiles/hbm_traffic.md"
 MFMA_UTIL_SOURCE = "profiles/mfma_utilisation.md"
 MFMA_UTIL = {
     "qproj_3b": {"proj_mfma": 0.028, "corr_quant": 0.065},
-    "downproj_8b": {"proj_mfma": 0.145, "corr_quant": 0.137},
-    "downproj_70b": {"proj_mfma": 0.341, "corr_quant": 0.300},
+    "downproj_8b": {"proj_mfma": 0.145, "corr_quant": 0.138},
+    "downproj_70b": {"proj_mfma": 0.337, "corr_quant": 0.295},
 }
 TRAFFIC_BYTES = {
     "downproj_8b": 1570.5e6,
