@@ -19,7 +19,7 @@ from dataclasses import dataclass
 import torch
 
 from narhip import ops
-from narhip.factors import _key, _remember, cached_prepared
+from narhip.factors import IdentityCache, cached_prepared
 
 from .r4_fused_v2 import (GROUP, PackedInt4, allocate_outputs, allocate_partial,  # noqa: F401
                           dequantize, reduce_partial, unpack)
@@ -106,21 +106,19 @@ TILE_CONFIGS = tuple(
 ) + tuple(TileConfig(block_t, warps, stages, use_dot=True)
           for block_t, warps, stages in ((16, 8, 3), (32, 8, 2), (64, 8, 2)))
 
-_FACTOR_FROM_TERMS: dict[tuple, torch.Tensor] = {}
+_FACTOR_FROM_TERMS = IdentityCache()
 
 
 def _factor_from_terms(y_padded: torch.Tensor, n: int, k: int, terms: int) -> torch.Tensor:
     """Sum of the first `terms` stacked bf16 terms -> fp32 [n, k] (exact for <= 3 terms)."""
-    key = (_key(y_padded), n, k, terms)
-    hit = _FACTOR_FROM_TERMS.get(key)
-    if hit is not None:
-        return hit
-    kp = y_padded.shape[1]
-    stacked = y_padded.reshape(-1, n, kp)[:terms, :, :k].float()
-    v = stacked[0].clone()
-    for t in range(1, terms):
-        v += stacked[t]
-    return _remember(_FACTOR_FROM_TERMS, key, v.contiguous())
+    def make() -> torch.Tensor:
+        kp = y_padded.shape[1]
+        stacked = y_padded.reshape(-1, n, kp)[:terms, :, :k].float()
+        v = stacked[0].clone()
+        for t in range(1, terms):
+            v += stacked[t]
+        return v.contiguous()
+    return _FACTOR_FROM_TERMS.get((y_padded,), (n, k, terms), make)
 
 
 def launch_projection_dot(x: torch.Tensor, y_padded: torch.Tensor, partial: torch.Tensor,

@@ -4,53 +4,91 @@ The reference prepares its factor terms once per factor set (FoldedR4.from_facto
 nar/fold_signed_permutation.py:70-114; NARDownTransform.__init__,
 quarot-llama3/nar_r4_kernel.py:225-243).  Call sites of the launcher API pass
 the raw fp32 factors on every call, so the derived device buffers (the [n, k]
-transpose of Y'^T and the prepared MFMA terms) are cached per source tensor,
-keyed by storage pointer, shape and version counter (an in-place update of the
-factor invalidates the entry).
+transpose of Y'^T and the prepared MFMA terms) are cached per source tensor.
+
+An entry is keyed by the identity of its source tensors, not by their storage
+address: it holds a weak reference to each source and a snapshot of the
+source's data pointer, shape, dtype, device and version counter, and it hits
+only while every source is the same live object with an unchanged snapshot.
+A finalizer drops the entry as soon as a source is garbage collected, so when
+a per-layer loop frees one layer's factors and the caching allocator hands
+their block to the next layer's factors (same address, version 0 again), the
+next lookup misses instead of returning the previous layer's terms.  A derived
+value never references its sources, so caching does not keep a factor alive.
 """
 
 from __future__ import annotations
+
+import weakref
+from typing import Callable, Sequence
 
 import torch
 
 from . import ops
 
-_TRANSPOSE: dict[tuple, torch.Tensor] = {}
-_PREPARED: dict[tuple, torch.Tensor] = {}
 _MAX_ENTRIES = 64
 
 
-def _key(t: torch.Tensor | None) -> tuple:
-    if t is None:
-        return (None,)
+def _state(t: torch.Tensor) -> tuple:
     return (t.data_ptr(), tuple(t.shape), t.dtype, str(t.device), t._version)
 
 
-def _remember(cache: dict, key: tuple, value: torch.Tensor) -> torch.Tensor:
-    if len(cache) >= _MAX_ENTRIES:
-        cache.pop(next(iter(cache)))
-    cache[key] = value
-    return value
+class IdentityCache:
+    """Derived tensors keyed by the identity (and unchanged state) of their sources."""
+
+    def __init__(self, max_entries: int = _MAX_ENTRIES):
+        self._entries: dict[tuple, tuple] = {}
+        self._max = max_entries
+
+    def __len__(self) -> int:
+        return len(self._entries)
+
+    def _drop(self, key: tuple) -> None:
+        entry = self._entries.pop(key, None)
+        if entry is not None:
+            for fin in entry[2]:
+                fin.detach()
+
+    def get(self, sources: Sequence[torch.Tensor | None], extra: tuple,
+            make: Callable[[], torch.Tensor]) -> torch.Tensor:
+        key = tuple(None if s is None else id(s) for s in sources) + tuple(extra)
+        entry = self._entries.get(key)
+        if entry is not None:
+            refs, states, _, value = entry
+            if all((s is None and r is None) or (s is not None and r is not None and r() is s and st == _state(s))
+                   for s, r, st in zip(sources, refs, states)):
+                return value
+            self._drop(key)
+        value = make()
+        refs = tuple(None if s is None else weakref.ref(s) for s in sources)
+        states = tuple(None if s is None else _state(s) for s in sources)
+        fins = tuple(weakref.finalize(s, self._drop, key) for s in sources if s is not None)
+        while len(self._entries) >= self._max:
+            self._drop(next(iter(self._entries)))
+        self._entries[key] = (refs, states, fins, value)
+        return value
+
+    def clear(self) -> None:
+        for key in list(self._entries):
+            self._drop(key)
+
+
+_TRANSPOSE = IdentityCache()
+_PREPARED = IdentityCache()
 
 
 def cached_transpose(y_t: torch.Tensor) -> torch.Tensor:
     """fp32 [k, n] -> contiguous fp32 [n, k]."""
-    key = _key(y_t)
-    hit = _TRANSPOSE.get(key)
-    if hit is not None:
-        return hit
-    return _remember(_TRANSPOSE, key, y_t.float().t().contiguous())
+    return _TRANSPOSE.get((y_t,), (), lambda: y_t.float().t().contiguous())
 
 
 def cached_prepared(v: torch.Tensor | None, w_t: torch.Tensor | None, n: int, k: int) -> torch.Tensor:
     """Prepared MFMA factor terms for (v, w_t); either half may be absent."""
-    key = (_key(v), _key(w_t), n, k)
-    hit = _PREPARED.get(key)
-    if hit is not None:
-        return hit
-    vv = None if v is None else v.float().contiguous()
-    ww = None if w_t is None else w_t.float().contiguous()
-    return _remember(_PREPARED, key, ops.prepare_rank_factors(vv, ww, n, k))
+    def make() -> torch.Tensor:
+        vv = None if v is None else v.float().contiguous()
+        ww = None if w_t is None else w_t.float().contiguous()
+        return ops.prepare_rank_factors(vv, ww, n, k)
+    return _PREPARED.get((v, w_t), (n, k), make)
 
 
 def clear() -> None:
