@@ -1,29 +1,25 @@
-// extern "C" boundary of libnarhip: argument validation, kernel selection and
-// launch.  See include/narhip.h for the contract of every entry point.
-#include "../../include/narhip.h"
-#include "narhip_device.hpp"
-#include "mfma.hpp"
-#include "rank_exact.hip"
-#include "rank_mfma.hip"
-#include "kron_mfma.hip"
-#include "rq_row.hip"
-#include "rq_seg.hip"
-#include "dequant.hip"
-#include "hooks.hip"
-#include "transform_f16.hip"
-#include "w4a4.hip"
+// extern "C" boundary of libnarhip: argument validation, planning and the
+// entry points of include/narhip.h.  The kernels are launched through the
+// launchers of host.hpp (launch_*.hip); this unit compiles no device code.
+#include "host.hpp"
 
-#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <map>
+#include <mutex>
 #include <string>
+#include <tuple>
 
 using namespace narhip;
+using namespace narhip::host;
+
+namespace narhip {
+namespace host {
 
 namespace {
-
 thread_local std::string g_error;
+}  // namespace
 
 int fail(int code, const char *fmt, ...)
 {
@@ -43,10 +39,26 @@ int check_launch(const char *what)
     return NARHIP_OK;
 }
 
-bool pow2(int64_t v) { return v > 0 && !(v & (v - 1)); }
-bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
-size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
-int round_up(int v, int m) { return (v + m - 1) / m * m; }
+const char *last_error() { return g_error.c_str(); }
+void clear_error() { g_error.clear(); }
+
+int64_t resident_blocks(const void *kernel, int threads, size_t lds)
+{
+    static std::mutex mu;
+    static std::map<std::tuple<const void *, int, size_t, int>, int64_t> cache;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+    const auto key = std::make_tuple(kernel, threads, lds, dev);
+    std::lock_guard<std::mutex> lock(mu);
+    auto it = cache.find(key);
+    if (it != cache.end()) return it->second;
+    int cus = 0, per = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1) cus = 256;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kernel, threads, lds) != hipSuccess || per < 1) per = 1;
+    const int64_t r = (int64_t)cus * per;
+    cache.emplace(key, r);
+    return r;
+}
 
 // ----------------------------------------------------------- Paley factors
 // Paley I construction: order m = p + 1 from the quadratic residues of a
@@ -119,318 +131,10 @@ PaleyTable paley_table(int m)
     return t;
 }
 
-float f32_sqrt(int v) { return (float)std::sqrt((double)v); }
+}  // namespace host
+}  // namespace narhip
 
-// Raise a kernel's dynamic LDS limit for blocks of 48 KB and more (the kernels
-// also hold a few KB of static LDS on top of the dynamic block).
-template <typename K>
-int set_lds(K kernel, size_t lds)
-{
-    if (lds < 48 * 1024) return NARHIP_OK;
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return fail(NARHIP_EHIP, "hipFuncSetAttribute: %s", hipGetErrorString(e));
-    return NARHIP_OK;
-}
-
-// ------------------------------------------------------- segment kernels
-
-template <int Q, int B>
-int launch_seg_qb(const SegArgs &a, int mode, hipStream_t s)
-{
-    const int64_t segs = a.T * (a.n / Q);
-    dim3 grid((unsigned)((segs + 15) / 16));
-    if (grid.x == 0) return NARHIP_OK;
-    switch (mode) {
-    case RANK_NONE: hipLaunchKernelGGL((rq_seg_kernel<Q, B, RANK_NONE, 0>), grid, dim3(256), 0, s, a); break;
-    case RANK_LOCAL: hipLaunchKernelGGL((rq_seg_kernel<Q, B, RANK_LOCAL, 8>), grid, dim3(256), 0, s, a); break;
-    default:
-        if (a.k <= 16) hipLaunchKernelGGL((rq_seg_kernel<Q, B, RANK_PARTIAL, 16>), grid, dim3(256), 0, s, a);
-        else hipLaunchKernelGGL((rq_seg_kernel<Q, B, RANK_PARTIAL, 64>), grid, dim3(256), 0, s, a);
-        break;
-    }
-    return check_launch("rq_seg_kernel");
-}
-
-template <int Q>
-int launch_seg_q(const SegArgs &a, int b, int mode, hipStream_t s)
-{
-    switch (b) {
-    case 32: return launch_seg_qb<Q, 32>(a, mode, s);
-    case 64: return launch_seg_qb<Q, 64>(a, mode, s);
-    case 128: return launch_seg_qb<Q, 128>(a, mode, s);
-    }
-    return fail(NARHIP_EUNSUPPORTED, "group %d not built", b);
-}
-
-int launch_seg(const SegArgs &a, int q, int b, int mode, hipStream_t s)
-{
-    switch (q) {
-    case 128: return launch_seg_q<128>(a, b, mode, s);
-    case 256: return launch_seg_q<256>(a, b, mode, s);
-    case 512: return launch_seg_q<512>(a, b, mode, s);
-    case 1024: return launch_seg_q<1024>(a, b, mode, s);
-    }
-    return fail(NARHIP_EUNSUPPORTED, "segment width %d not built", q);
-}
-
-// ------------------------------------------------------ Kronecker kernels
-
-template <int M, int Q, int B>
-int launch_row_mqb(const RowArgs &a, hipStream_t s)
-{
-    const size_t lds = sizeof(float) * M * Q;
-    if (int rc = set_lds(&rq_row_kernel<M, Q, B>, lds)) return rc;
-    hipLaunchKernelGGL((rq_row_kernel<M, Q, B>), dim3((unsigned)a.T), dim3(256), lds, s, a);
-    return check_launch("rq_row_kernel");
-}
-
-// Grid of a persistent kernel: as many workgroups as fit on the device at
-// once (occupancy at this block size and LDS), at most `work`.  Cached per
-// kernel and device.
-template <typename K>
-int64_t persistent_grid(K kernel, int threads, size_t lds, int64_t work)
-{
-    static thread_local int cached_dev = -1;
-    static thread_local int64_t cached = 0;
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) dev = 0;
-    if (dev != cached_dev) {
-        int cus = 0, per = 0;
-        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1) cus = 256;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, reinterpret_cast<const void *>(kernel), threads, lds) !=
-                hipSuccess || per < 1)
-            per = 1;
-        cached = (int64_t)cus * per;
-        cached_dev = dev;
-    }
-    return cached < work ? cached : work;
-}
-
-template <int M, int Q, int B>
-int launch_kron_mqb(const KronArgs &a, bool quant, hipStream_t s)
-{
-    const size_t lds = sizeof(float) * kron_rows<M>() * (Q + KPAD);
-    constexpr bool persist = Q >= 1024;   // 115 KB of LDS: one workgroup per CU
-    if (quant) {
-        auto k = &kron_mfma_kernel<M, Q, B, true, persist>;
-        if (int rc = set_lds(k, lds)) return rc;
-        const int64_t grid = persist ? persistent_grid(k, 16 * M, lds, a.T) : a.T;
-        hipLaunchKernelGGL((kron_mfma_kernel<M, Q, B, true, persist>), dim3((unsigned)grid), dim3(16 * M), lds, s, a);
-    } else {
-        auto k = &kron_mfma_kernel<M, Q, 128, false, persist>;
-        if (int rc = set_lds(k, lds)) return rc;
-        const int64_t grid = persist ? persistent_grid(k, 16 * M, lds, a.T) : a.T;
-        hipLaunchKernelGGL((kron_mfma_kernel<M, Q, 128, false, persist>), dim3((unsigned)grid), dim3(16 * M), lds, s, a);
-    }
-    return check_launch("kron_mfma_kernel");
-}
-
-// exact: rq_row (fp64 Paley) with RowArgs; otherwise kron_mfma with KronArgs
-template <int M, int Q>
-int launch_kron_mq(const RowArgs *ra, const KronArgs *ka, bool quant, int b, hipStream_t s)
-{
-    switch (b) {
-    case 32: return ra ? launch_row_mqb<M, Q, 32>(*ra, s) : launch_kron_mqb<M, Q, 32>(*ka, quant, s);
-    case 64: return ra ? launch_row_mqb<M, Q, 64>(*ra, s) : launch_kron_mqb<M, Q, 64>(*ka, quant, s);
-    case 128: return ra ? launch_row_mqb<M, Q, 128>(*ra, s) : launch_kron_mqb<M, Q, 128>(*ka, quant, s);
-    }
-    return fail(NARHIP_EUNSUPPORTED, "group %d not built", b);
-}
-
-template <int M>
-int launch_kron_m(const RowArgs *ra, const KronArgs *ka, bool quant, int q, int b, hipStream_t s)
-{
-    switch (q) {
-    case 256: return launch_kron_mq<M, 256>(ra, ka, quant, b, s);
-    case 512: return launch_kron_mq<M, 512>(ra, ka, quant, b, s);
-    case 1024: return launch_kron_mq<M, 1024>(ra, ka, quant, b, s);
-    }
-    return fail(NARHIP_EUNSUPPORTED, "Kronecker H_%d x H_%d not built", M, q);
-}
-
-int launch_kron(const RowArgs *ra, const KronArgs *ka, bool quant, int m, int q, int b, hipStream_t s)
-{
-    if (m == 12) return launch_kron_m<12>(ra, ka, quant, q, b, s);
-    if (m == 28) return launch_kron_m<28>(ra, ka, quant, q, b, s);
-    return fail(NARHIP_EUNSUPPORTED, "Paley order %d not built", m);
-}
-
-// ------------------------------------------------------------ rank kernels
-
-int launch_proj_exact(const uint16_t *x, int64_t T, int64_t n, int64_t ldx, const float *v,
-                      int k, int splits, float *partial, hipStream_t s)
-{
-    if (T == 0) return NARHIP_OK;
-    ProjArgs a{x, ldx, T, n, v, partial, k, splits};
-    hipLaunchKernelGGL(proj_exact_kernel, dim3((unsigned)((T + 31) / 32), (unsigned)splits), dim3(256), 0, s, a);
-    return check_launch("proj_exact_kernel");
-}
-
-int launch_corr_exact(const float *partial, int splits, int k, const float *wt, int64_t T, int64_t n,
-                      float *corr, hipStream_t s)
-{
-    if (T == 0) return NARHIP_OK;
-    CorrArgs a{partial, splits, k, wt, T, n, corr};
-    hipLaunchKernelGGL(corr_exact_kernel, dim3((unsigned)((T + 31) / 32), (unsigned)(n / 64)), dim3(256), 0, s, a);
-    return check_launch("corr_exact_kernel");
-}
-
-// Prepared factor layout: vt [3][kp16][n] bf16, then wtt [3][n][kp32] bf16.
-int kp16(int k) { return round_up(k < 1 ? 1 : k, 16); }
-int kp32(int k) { return round_up(k < 1 ? 1 : k, 32); }
-size_t vt_bytes(int64_t n, int k) { return align256(sizeof(uint16_t) * 3 * (size_t)kp16(k) * (size_t)n); }
-size_t wtt_bytes(int64_t n, int k) { return align256(sizeof(uint16_t) * 3 * (size_t)kp32(k) * (size_t)n); }
-size_t prepared_bytes(int64_t n, int k) { return vt_bytes(n, k) + wtt_bytes(n, k); }
-
-int launch_prepare(const float *v, const float *wt, int64_t n, int k, void *prep, hipStream_t s)
-{
-    __bf16 *vt = static_cast<__bf16 *>(prep);
-    __bf16 *wtt = reinterpret_cast<__bf16 *>(static_cast<char *>(prep) + vt_bytes(n, k));
-    if (v) {
-        const int64_t nv = n * kp16(k);
-        hipLaunchKernelGGL(prep_v_kernel, dim3((unsigned)((nv + 255) / 256)), dim3(256), 0, s, v, n, k, kp16(k), vt);
-        if (int rc = check_launch("prep_v_kernel")) return rc;
-    }
-    if (wt) {
-        const int64_t nw = n * kp32(k);
-        hipLaunchKernelGGL(prep_w_kernel, dim3((unsigned)((nw + 255) / 256)), dim3(256), 0, s, wt, n, k, kp32(k), wtt);
-        if (int rc = check_launch("prep_w_kernel")) return rc;
-    }
-    return NARHIP_OK;
-}
-
-// Splits of the fp64 VALU projection (16-token tiles): about 1024 workgroups,
-// each split a whole number of 128-channel blocks.
-int f64_splits(int64_t T, int64_t n)
-{
-    const int64_t tiles = (T + 15) / 16;
-    int s = 1;
-    while (s < 64 && tiles * s * 2 <= 1024 && n % (128 * 2 * (int64_t)s) == 0) s *= 2;
-    return s;
-}
-int f64_kmax(int k) { return k <= 8 ? 8 : 16; }
-
-int launch_proj_f64(const uint16_t *x, int64_t T, int64_t n, int64_t ldx, const float *v, int k, int splits,
-                    double *pd, hipStream_t s, bool f16 = false, float *pf = nullptr)
-{
-    if (T == 0) return NARHIP_OK;
-    ProjF64Args a{x, ldx, T, n, v, pd, k, splits, pf};
-    dim3 grid((unsigned)((T + 15) / 16), (unsigned)splits);
-    if (f16) {
-        if (k <= 8) hipLaunchKernelGGL((proj_f64_kernel<8, true>), grid, dim3(256), 0, s, a);
-        else hipLaunchKernelGGL((proj_f64_kernel<16, true>), grid, dim3(256), 0, s, a);
-    } else {
-        if (k <= 8) hipLaunchKernelGGL((proj_f64_kernel<8>), grid, dim3(256), 0, s, a);
-        else hipLaunchKernelGGL((proj_f64_kernel<16>), grid, dim3(256), 0, s, a);
-    }
-    return check_launch("proj_f64_kernel");
-}
-
-int launch_fold_f64(const double *pd, int splits, int kmax, int k, int64_t T, float *u, hipStream_t s)
-{
-    const int64_t n = T * k;
-    hipLaunchKernelGGL(fold_f64_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, pd, splits, kmax, k, T, u);
-    return check_launch("fold_f64_kernel");
-}
-
-int launch_fold_f32(const float *partial, int splits, int k, int64_t T, float *u, hipStream_t s)
-{
-    const int64_t n = T * k;
-    hipLaunchKernelGGL(fold_f32_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, partial, splits, k, T, u);
-    return check_launch("fold_f32_kernel");
-}
-
-// Channel splits for the MFMA projection: enough workgroups for two per CU
-// (128-token tiles, splits of a multiple of 128 channels).
-int mfma_splits(int64_t T, int64_t n)
-{
-    const int64_t tiles = (T + 127) / 128;
-    int s = 1;
-    while (s < 64 && tiles * s < 512 && n % (128 * 2 * (int64_t)s) == 0) s *= 2;
-    return s;
-}
-
-bool mfma_projection_ok(int64_t n, int splits) { return n % (128 * (int64_t)splits) == 0; }
-
-int launch_proj_mfma(const uint16_t *x, int64_t T, int64_t n, int64_t ldx, const void *prep, int k, int splits,
-                     float *partial, hipStream_t s)
-{
-    if (T == 0) return NARHIP_OK;
-    if (!mfma_projection_ok(n, splits))
-        return fail(NARHIP_EUNSUPPORTED, "MFMA projection needs n %% (128*splits) == 0 (n=%lld, splits=%d)",
-                    (long long)n, splits);
-    ProjMfmaArgs a{x, ldx, T, n, static_cast<const __bf16 *>(prep), kp16(k), k, splits, n / splits, partial};
-    dim3 grid((unsigned)((T + 127) / 128), (unsigned)splits);
-    switch (kp16(k) / 16) {
-    case 1: hipLaunchKernelGGL((proj_mfma_kernel<1>), grid, dim3(256), 0, s, a); break;
-    case 2: hipLaunchKernelGGL((proj_mfma_kernel<2>), grid, dim3(256), 0, s, a); break;
-    case 3: hipLaunchKernelGGL((proj_mfma_kernel<3>), grid, dim3(256), 0, s, a); break;
-    case 4: hipLaunchKernelGGL((proj_mfma_kernel<4>), grid, dim3(256), 0, s, a); break;
-    default: return fail(NARHIP_EUNSUPPORTED, "rank %d", k);
-    }
-    return check_launch("proj_mfma_kernel");
-}
-
-// A second stream per device (default priority, non-blocking) with a fork and a
-// join event, created on first use by each host thread and kept for the
-// process.  The full-row rank path runs the projection (and the fold of its
-// partials) on it, concurrently with the Kronecker transform on the caller's
-// stream: the transform is VALU-bound, the projection waits on memory.
-int launch_fold_u(const float *partial, int splits, int k, int kp, int64_t T, __bf16 *u3, hipStream_t s)
-{
-    const int64_t n = T * kp;
-    hipLaunchKernelGGL(fold_u_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, partial, splits, k, kp, T, u3);
-    return check_launch("fold_u_kernel");
-}
-
-// u terms [T][3][kp32] bf16, then a scratch row of n/2 bytes for the stores of
-// out-of-range tokens of the last tile (n/2 + 4 KB: codes, scales, rotated x')
-size_t u3_bytes(int64_t T, int k) { return sizeof(uint16_t) * 3 * (size_t)kp32(k) * (size_t)T; }
-size_t corr_scratch_bytes(int64_t T, int64_t n, int k) { return align256(u3_bytes(T, k)) + align256((size_t)n / 2 + 4096); }
-
-template <int B, int KS, int CW>
-int launch_cq(const CorrQuantArgs &a, dim3 grid, hipStream_t s)
-{
-    if (a.rotated) hipLaunchKernelGGL((corr_quant_kernel<B, KS, CW, true>), grid, dim3(256), 0, s, a);
-    else hipLaunchKernelGGL((corr_quant_kernel<B, KS, CW, false>), grid, dim3(256), 0, s, a);
-    return check_launch("corr_quant_kernel");
-}
-
-template <int B>
-int launch_cq_b(const CorrQuantArgs &a, int ks, int cw, dim3 grid, hipStream_t s)
-{
-    if (ks == 1 && cw == 256) return launch_cq<B, 1, 256>(a, grid, s);
-    if (ks == 1) return launch_cq<B, 1, 128>(a, grid, s);
-    return launch_cq<B, 2, 128>(a, grid, s);
-}
-
-// Workgroups own 48 KB of W^T terms (256 channels at k <= 32, else 128) and
-// run enough 128-token tiles over them that about 1024 workgroups remain.
-int launch_corr_quant(CorrQuantArgs a, int b, hipStream_t s)
-{
-    if (a.T == 0) return NARHIP_OK;
-    const int ks = a.kp / 32;
-    // 256 channels (48 KB of W^T terms) per workgroup where the register tile
-    // of two groups fits (b <= 64, k <= 32); else one 128-channel block
-    const int cw = (ks == 1 && b <= 64 && a.n % 256 == 0) ? 256 : 128;
-    if (a.n % cw || cw % b) return fail(NARHIP_EUNSUPPORTED, "rank correction needs n %% 128 == 0");
-    a.ncb = a.n / cw;
-    const int64_t tiles = (a.T + 127) / 128;
-    int tpw = 1;
-    while (tpw < 8 && a.ncb * ((tiles + 2 * tpw - 1) / (2 * tpw)) >= 1024) tpw *= 2;
-    a.tpw = tpw;
-    const int64_t groups = (tiles + tpw - 1) / tpw;
-    const int64_t blocks = 8 * a.ncb * ((groups + 7) / 8);
-    if (blocks > 0x7fffffff) return fail(NARHIP_EUNSUPPORTED, "too many tokens");
-    dim3 grid((unsigned)blocks);
-    switch (b) {
-    case 32: return launch_cq_b<32>(a, ks, cw, grid, s);
-    case 64: return launch_cq_b<64>(a, ks, cw, grid, s);
-    case 128: return launch_cq_b<128>(a, ks, cw, grid, s);
-    }
-    return fail(NARHIP_EUNSUPPORTED, "group %d not built", b);
-}
+namespace {
 
 // --------------------------------------------------------------- planning
 
@@ -454,59 +158,6 @@ int64_t chunk_tokens(int64_t T, int64_t n)
     return tc < T ? tc : T;
 }
 
-// fp16 transform at q = 128, k <= 8: proj_tok (unless the caller brings
-// partials) + xform128, which folds the chunk sums itself.
-bool xf_fast(int32_t had_q, int32_t k) { return had_q == 128 && k >= 1 && k <= XF_K; }
-
-// Channel chunks per projection block: the smallest divisor S of n/128 that
-// gives >= 512 blocks of 64 tokens (all of them when none does; measured:
-// 512 rather than 1024 saves 5 us at 2048 x 14336).
-int xf_splits(int64_t T, int64_t n)
-{
-    const int64_t nb = n / 128, tiles = (T + 63) / 64;
-    for (int64_t d = 1; d <= nb; d++)
-        if (nb % d == 0 && tiles * d >= 512) return (int)d;
-    return (int)nb;
-}
-
-size_t xf_pd_bytes(int64_t T, int S) { return align256(sizeof(double) * XF_K * (size_t)T * (size_t)S); }
-
-int launch_proj_tok(const uint16_t *x, int64_t T, int64_t n, int64_t ldx, const float *v, int k, int S,
-                    double *pd, float *pf, hipStream_t s, bool f16 = true)
-{
-    ProjTokArgs a{x, ldx, T, n, v, pd, pf, k, S, k % 4 == 0 && aligned16(v)};
-    const dim3 grid((unsigned)((T + 63) / 64), (unsigned)S);
-    if (f16) hipLaunchKernelGGL(proj_tok_kernel<true>, grid, dim3(256), 0, s, a);
-    else hipLaunchKernelGGL(proj_tok_kernel<false>, grid, dim3(256), 0, s, a);
-    return check_launch("proj_tok_kernel");
-}
-
-// u from proj_tok's chunk sums pd [T][S][XF_K], or from the caller's fp32
-// partials pf [T][S*k].  quant != null: bf16 rows, INT4 group-128 outputs
-// (codes, scales, zeros, dest and signs from *quant); else fp16 rows to fp16 `out`.
-int launch_xform128(const uint16_t *x, int64_t T, int64_t n, int64_t ldx, const float *w_t, const double *pd,
-                    const float *pf, int S, int k, uint16_t *out, hipStream_t s, const XformArgs *quant = nullptr)
-{
-    // ~2048 workgroups, but at least 32 tokens each (each loads 64 KB of W^T
-    // before its first token) while that still leaves >= 512 workgroups
-    const int64_t gx = (n / 128 + 15) / 16;
-    int64_t gy = (2048 + gx - 1) / gx;
-    if (T < 32 * gy) {
-        const int64_t lo = (512 + gx - 1) / gx;
-        gy = (T + 31) / 32 > lo ? (T + 31) / 32 : lo;
-    }
-    if (gy > T) gy = T;
-    const int64_t tpb = (T + gy - 1) / gy;
-    gy = (T + tpb - 1) / tpb;
-    XformArgs a = quant ? *quant : XformArgs{};
-    a.x = x; a.ldx = ldx; a.T = T; a.n = n; a.wt = w_t; a.pd = pd; a.pf = pf; a.S = S; a.out = out; a.k = k; a.tpb = (int)tpb;
-    a.sq = f32_sqrt(128);
-    a.rsq = 1.0f / a.sq;
-    const dim3 grid((unsigned)gx, (unsigned)gy);
-    if (quant) hipLaunchKernelGGL(xform128_kernel<true>, grid, dim3(256), 0, s, a);
-    else hipLaunchKernelGGL(xform128_kernel<false>, grid, dim3(256), 0, s, a);
-    return check_launch("xform128_kernel");
-}
 
 
 struct Plan {
@@ -611,7 +262,10 @@ int run_rotate_quant(const void *x_bf16, int64_t T, int64_t n, int64_t ldx, int 
     if (!aligned16(x_bf16) || !aligned16(codes) || (rotated && !aligned16(rotated)) || !aligned16(prepared) ||
         !aligned16(wt))
         return fail(NARHIP_EINVAL, "x, codes, rotated, prepared and w_t must be 16-byte aligned");
-    if (k > 0 && p.path != PATH_SEG && !prepared && !wt) return fail(NARHIP_EINVAL, "rank factor w_t missing");
+    // only the MFMA rank path reads the prepared W^T terms; every other path
+    // with a rank term reads w_t itself
+    if (k > 0 && p.path != PATH_SEG && !wt && !(p.path == PATH_MFMA_RANK && prepared))
+        return fail(NARHIP_EINVAL, "rank factor w_t missing");
     if (k > 0 && (p.need_proj || p.seg_mode == RANK_LOCAL) && !v && !(p.path == PATH_MFMA_RANK && prepared))
         return fail(NARHIP_EINVAL, "rank factor v missing");
     if (p.seg_mode == RANK_LOCAL && (!v || !wt)) return fail(NARHIP_EINVAL, "rank factors missing");
@@ -741,7 +395,7 @@ extern "C" {
 
 int narhip_abi_version(void) { return NARHIP_ABI_VERSION; }
 
-const char *narhip_last_error_string(void) { return g_error.c_str(); }
+const char *narhip_last_error_string(void) { return last_error(); }
 
 int narhip_paley(int32_t m, int8_t *out_host)
 {
@@ -761,7 +415,7 @@ size_t narhip_rank_factors_bytes(int64_t n, int32_t k)
 int narhip_prepare_rank_factors(const float *v, const float *w_t, int64_t n, int32_t k, void *prepared,
                                 size_t prepared_bytes_given, void *stream)
 {
-    g_error.clear();
+    clear_error();
     if (n <= 0 || k < 1 || k > 64) return fail(NARHIP_EINVAL, "bad shape n=%lld k=%d", (long long)n, k);
     if (!prepared || !aligned16(prepared)) return fail(NARHIP_EINVAL, "prepared buffer missing or misaligned");
     if (prepared_bytes_given < prepared_bytes(n, k))
@@ -789,7 +443,7 @@ int narhip_rotate_quant(const void *x_bf16, int64_t tokens, int64_t n, int64_t l
                         float *rotated, const int64_t *dest_rows, int32_t rank_mode,
                         void *workspace, size_t workspace_bytes, void *stream)
 {
-    g_error.clear();
+    clear_error();
     return run_rotate_quant(x_bf16, tokens, n, ld_x, had_m, had_q, signs, k, rank_block, v, w_t, prepared,
                             partial, splits, group, codes, scales_f16, zeros_f16, rotated, dest_rows, rank_mode,
                             workspace, workspace_bytes, static_cast<hipStream_t>(stream));
@@ -799,7 +453,7 @@ int narhip_rank_projection(const void *x_bf16, int64_t tokens, int64_t n, int64_
                            const float *v, const void *prepared, int32_t k, int32_t splits, float *partial,
                            int32_t rank_mode, void *stream)
 {
-    g_error.clear();
+    clear_error();
     if (tokens < 0 || n <= 0 || ld_x < n || ld_x % 8) return fail(NARHIP_EINVAL, "bad shape");
     if (k < 1 || k > 64) return fail(NARHIP_EUNSUPPORTED, "rank k=%d outside [1, 64]", k);
     if (splits < 1 || n % splits) return fail(NARHIP_EINVAL, "%lld channels do not divide into %d splits",
@@ -823,7 +477,7 @@ int narhip_group_quant(const void *x_bf16, int64_t tokens, int64_t n, int64_t ld
                        uint8_t *codes, void *scales_f16, void *zeros_f16, int32_t rank_mode,
                        void *workspace, size_t workspace_bytes, void *stream)
 {
-    g_error.clear();
+    clear_error();
     if (k > 0 && !partial) return fail(NARHIP_EINVAL, "partials required");
     return run_rotate_quant(x_bf16, tokens, n, ld_x, had_m, had_q, nullptr, k, n, nullptr, w_t, prepared, partial,
                             splits, group, codes, scales_f16, zeros_f16, nullptr, nullptr, rank_mode,
@@ -833,24 +487,21 @@ int narhip_group_quant(const void *x_bf16, int64_t tokens, int64_t n, int64_t ld
 int narhip_dequantize(const uint8_t *codes, const void *scales_f16, const void *zeros_f16,
                       int64_t rows, int64_t n, int32_t group, float *out, void *stream)
 {
-    g_error.clear();
+    clear_error();
     if (rows < 0 || n <= 0 || group <= 0 || n % group || group % 8)
         return fail(NARHIP_EINVAL, "bad shape rows=%lld n=%lld group=%d", (long long)rows, (long long)n, group);
     if (rows == 0) return NARHIP_OK;
     if (!codes || !scales_f16 || !zeros_f16 || !out) return fail(NARHIP_EINVAL, "null tensor argument");
     if (!aligned16(out) || (reinterpret_cast<uintptr_t>(codes) & 3u))
         return fail(NARHIP_EINVAL, "codes must be 4-byte and out 16-byte aligned");
-    const int64_t words = rows * n / 8;
-    hipLaunchKernelGGL(dequant_kernel, dim3((unsigned)((words + 255) / 256)), dim3(256), 0,
-                       static_cast<hipStream_t>(stream), codes, static_cast<const uint16_t *>(scales_f16),
-                       static_cast<const uint16_t *>(zeros_f16), rows, n, group, out);
-    return check_launch("dequant_kernel");
+    return launch_dequant(codes, static_cast<const uint16_t *>(scales_f16), static_cast<const uint16_t *>(zeros_f16),
+                          rows, n, group, out, static_cast<hipStream_t>(stream));
 }
 
 int narhip_dynamic_asym_int4(const void *x, int32_t dtype, int64_t rows, int64_t n, int32_t group,
                              uint8_t *codes, void *scales_f16, void *zeros_f16, void *deq, void *stream)
 {
-    g_error.clear();
+    clear_error();
     if (rows < 0 || n <= 0) return fail(NARHIP_EINVAL, "bad shape rows=%lld n=%lld", (long long)rows, (long long)n);
     if (group <= 0 || n % group)
         return fail(NARHIP_EINVAL, "last dimension %lld is not divisible by group size %d", (long long)n, group);
@@ -861,22 +512,14 @@ int narhip_dynamic_asym_int4(const void *x, int32_t dtype, int64_t rows, int64_t
     if (!x || !codes || !scales_f16 || !zeros_f16 || !deq) return fail(NARHIP_EINVAL, "null tensor argument");
     if (!aligned16(x) || !aligned16(deq) || (reinterpret_cast<uintptr_t>(codes) & 7u))
         return fail(NARHIP_EINVAL, "x and deq must be 16-byte aligned, codes 8-byte aligned");
-    const int64_t elems = rows * n;
-    dim3 grid((unsigned)((elems / 8 + 255) / 256));
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    uint16_t *sc = static_cast<uint16_t *>(scales_f16), *zc = static_cast<uint16_t *>(zeros_f16);
-    switch (dtype) {
-    case DT_F32: hipLaunchKernelGGL(quant_tuple_kernel<DT_F32>, grid, dim3(256), 0, s, x, elems, group, codes, sc, zc, deq); break;
-    case DT_BF16: hipLaunchKernelGGL(quant_tuple_kernel<DT_BF16>, grid, dim3(256), 0, s, x, elems, group, codes, sc, zc, deq); break;
-    default: hipLaunchKernelGGL(quant_tuple_kernel<DT_F16>, grid, dim3(256), 0, s, x, elems, group, codes, sc, zc, deq); break;
-    }
-    return check_launch("quant_tuple_kernel");
+    return launch_quant_tuple(dtype, x, rows * n, group, codes, static_cast<uint16_t *>(scales_f16),
+                              static_cast<uint16_t *>(zeros_f16), deq, static_cast<hipStream_t>(stream));
 }
 
 int narhip_hadamard_rows(const void *x_bf16, int64_t rows, int64_t n, int64_t ld_x, int32_t had_m, int32_t had_q,
                          const float *signs, float *out, void *stream)
 {
-    g_error.clear();
+    clear_error();
     if (rows < 0 || n <= 0) return fail(NARHIP_EINVAL, "bad shape rows=%lld n=%lld", (long long)rows, (long long)n);
     if (!pow2(had_q) || had_q < 128 || had_q > 1024)
         return fail(NARHIP_EUNSUPPORTED, "Hadamard block width %d: need a power of two in [128, 1024]", had_q);
@@ -918,7 +561,7 @@ size_t narhip_transform_f16_workspace(int64_t tokens, int64_t n, int32_t k)
 int narhip_rank_projection_f16(const void *x_f16, int64_t tokens, int64_t n, int64_t ld_x, const float *v,
                                int32_t k, int32_t splits, float *partial, void *stream)
 {
-    g_error.clear();
+    clear_error();
     if (tokens < 0 || n <= 0 || ld_x < n || ld_x % 8) return fail(NARHIP_EINVAL, "bad shape");
     if (k < 1 || k > 16) return fail(NARHIP_EUNSUPPORTED, "fp16 projection supports rank k in [1, 16] (got %d)", k);
     if (splits < 1 || n % splits || (n / splits) % 2)
@@ -934,7 +577,7 @@ int narhip_transform_f16(const void *x_f16, int64_t tokens, int64_t n, int64_t l
                          const float *v, const float *partial, int32_t splits, const float *w_t, int32_t k,
                          void *out_f16, void *workspace, size_t workspace_bytes, void *stream)
 {
-    g_error.clear();
+    clear_error();
     if (tokens < 0 || n <= 0) return fail(NARHIP_EINVAL, "bad shape tokens=%lld n=%lld", (long long)tokens, (long long)n);
     if (!pow2(had_q) || had_q < 128 || had_q > 1024 || n % had_q)
         return fail(NARHIP_EUNSUPPORTED, "block Hadamard width %d must be a power of two in [128, 1024] dividing n",
@@ -981,19 +624,7 @@ int narhip_transform_f16(const void *x_f16, int64_t tokens, int64_t n, int64_t l
     a.wt = w_t; a.k = k;
     a.codes = nullptr; a.rotated = static_cast<float *>(out_f16);
     a.sq = f32_sqrt(had_q); a.rsq = 1.0f / a.sq;
-    const int64_t segs = tokens * (n / had_q);
-    dim3 grid((unsigned)((segs + 15) / 16));
-#define NARHIP_F16_SEG(QQ)                                                                                      \
-    if (k > 0) hipLaunchKernelGGL((rq_seg_kernel<QQ, 128, RANK_PARTIAL, 16, true>), grid, dim3(256), 0, s, a); \
-    else hipLaunchKernelGGL((rq_seg_kernel<QQ, 128, RANK_NONE, 0, true>), grid, dim3(256), 0, s, a);
-    switch (had_q) {
-    case 128: NARHIP_F16_SEG(128) break;
-    case 256: NARHIP_F16_SEG(256) break;
-    case 512: NARHIP_F16_SEG(512) break;
-    default: NARHIP_F16_SEG(1024) break;
-    }
-#undef NARHIP_F16_SEG
-    return check_launch("rq_seg_kernel (fp16)");
+    return launch_seg_f16(a, had_q, k, s);
 }
 
 namespace {
@@ -1021,7 +652,7 @@ int narhip_w4a4_gemm(const uint8_t *a_codes, const void *a_scales, const void *a
                      int64_t n, int32_t group, float *out, int64_t ld_out, void *workspace, size_t workspace_bytes,
                      void *stream)
 {
-    g_error.clear();
+    clear_error();
     if (tokens < 0 || out_features < 0 || n <= 0)
         return fail(NARHIP_EINVAL, "bad shape tokens=%lld out_features=%lld n=%lld", (long long)tokens,
                     (long long)out_features, (long long)n);
@@ -1047,22 +678,15 @@ int narhip_w4a4_gemm(const uint8_t *a_codes, const void *a_scales, const void *a
     W4A4Args a{a_codes, static_cast<const uint16_t *>(a_scales), static_cast<const uint16_t *>(a_zeros), tokens,
                w_codes, static_cast<const uint16_t *>(w_scales), static_cast<const uint16_t *>(w_zeros),
                out_features, n, part, ld_out, splits};
-    hipLaunchKernelGGL(w4a4_kernel, dim3((unsigned)gx, (unsigned)gy, (unsigned)splits), dim3(256), 0, s, a);
-    int rc = check_launch("w4a4_kernel");
-    if (rc || splits == 1) return rc;
-    const int64_t cnt = tokens * out_features;
-    hipLaunchKernelGGL(w4a4_reduce_kernel, dim3((unsigned)((cnt + 255) / 256)), dim3(256), 0, s, part, splits, tokens,
-                       out_features, out, ld_out);
-    return check_launch("w4a4_reduce_kernel");
+    return launch_w4a4(a, gx, gy, out, s);
 }
 
 int narhip_mfma_probe(const void *a_bf16, const void *b_bf16, float *d, void *stream)
 {
-    g_error.clear();
+    clear_error();
     if (!a_bf16 || !b_bf16 || !d) return fail(NARHIP_EINVAL, "null argument");
-    hipLaunchKernelGGL(mfma_probe_kernel, dim3(1), dim3(64), 0, static_cast<hipStream_t>(stream),
-                       static_cast<const __bf16 *>(a_bf16), static_cast<const __bf16 *>(b_bf16), d);
-    return check_launch("mfma_probe_kernel");
+    return launch_mfma_probe(static_cast<const __bf16 *>(a_bf16), static_cast<const __bf16 *>(b_bf16), d,
+                             static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

@@ -1,11 +1,13 @@
 // Dequantization of the packed INT4 layout: out = q * s + z, computed as an
 // fp32 multiply followed by an fp32 add (no fused multiply-add), as
 // nar/kernels/r4_fused_v2.py:364-369 and nar/experiment.py:183 do.
+#pragma once
 #include "narhip_device.hpp"
 
 namespace narhip {
 
 // One thread per 8 channels (one 32-bit word of codes).
+template <int = 0>
 __global__ void __launch_bounds__(256)
 dequant_kernel(const uint8_t *codes, const uint16_t *scales, const uint16_t *zeros,
                int64_t rows, int64_t n, int group, float *out)

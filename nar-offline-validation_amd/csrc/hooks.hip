@@ -7,6 +7,7 @@
 // min/max, raw = (hi - lo) / 15, both degenerate-group guards, fp16 RNE of scale
 // and zero, q = clamp(round_half_even(RN(x - z) / s), 0, 15), deq = RN(q * s) + z
 // rounded once to the input dtype.
+#pragma once
 #include "narhip_device.hpp"
 
 namespace narhip {
@@ -77,13 +78,13 @@ quant_tuple_kernel(const void *x, int64_t elems, int group, uint8_t *codes, uint
     const int64_t c = ok ? chunk : nchunks - 1;
     float v[8];
     load8<DT>(x, c * 8, v);
-    float lo = v[0], hi = v[0];
-#pragma unroll
-    for (int e = 1; e < 8; e++) { lo = fminf(lo, v[e]); hi = fmaxf(hi, v[e]); }
+    // torch.amin / torch.amax semantics: a NaN anywhere in the group wins
+    float lo, hi;
+    lane_minmax_nan<8>(v, lo, hi);
     const int lanes = group / 8;
     for (int off = 1; off < lanes; off <<= 1) {
-        lo = fminf(lo, __shfl_xor(lo, off));
-        hi = fmaxf(hi, __shfl_xor(hi, off));
+        lo = min_nan(lo, __shfl_xor(lo, off));
+        hi = max_nan(hi, __shfl_xor(hi, off));
     }
     const GroupParams g = group_params(lo, hi);
     uint32_t q[8];
@@ -91,7 +92,10 @@ quant_tuple_kernel(const void *x, int64_t elems, int group, uint8_t *codes, uint
 #pragma unroll
     for (int e = 0; e < 8; e++) {
         q[e] = quant_code(v[e], g);
-        d[e] = __fadd_rn(__fmul_rn((float)q[e], g.s), g.z);
+        // the reference dequantizes the clamped float quotient, which stays NaN
+        // where (x - z) / s is NaN (Inf - Inf, Inf / Inf); its uint8 code is 0
+        const float quo = __builtin_rintf((v[e] - g.z) / g.s);
+        d[e] = quo != quo ? quo : __fadd_rn(__fmul_rn((float)q[e], g.s), g.z);
     }
     if (!ok) return;
     const uint32_t lo4 = q[0] | (q[1] << 8) | (q[2] << 16) | (q[3] << 24);

@@ -9,6 +9,7 @@
 //            reference's BLAS product -- whenever the two sums are exact in fp32.
 //   phase 3  either the group quantizer (no rank term) or a coalesced copy of P
 //            to global memory for the rank-k correction kernel.
+#pragma once
 #include "mfma.hpp"
 #include "narhip_device.hpp"
 
@@ -183,7 +184,13 @@ kron_mfma_kernel(KronArgs a)
                     // padded rows get an exact +0, whatever the column held: an
                     // Inf or NaN of this token must not reach the next token's
                     // Paley stage through 0 * NaN
-                    const float p = __builtin_fmaf(hm, s1[i], hm * s2[i]);
+                    // An infinite F value splits into (Inf, NaN, NaN): s1 then
+                    // carries the IEEE sum (+-Inf, or NaN for Inf - Inf) and s2 is
+                    // NaN.  The median with +-FLT_MAX returns a NaN operand's
+                    // minimum (-FLT_MAX), so a NaN s2 leaves hm * s1 alone;
+                    // finite products pass unchanged.
+                    const float s2c = __builtin_amdgcn_fmed3f(hm * s2[i], -0x1.fffffep+127f, 0x1.fffffep+127f);
+                    const float p = __builtin_fmaf(hm, s1[i], s2c);
                     if (PAD) F[widx(mt, i)] = ar < M ? p : 0.0f;
                     else if (ar < M) F[widx(mt, i)] = p;
                 }
@@ -265,12 +272,8 @@ kron_mfma_kernel(KronArgs a)
                 v[0] = p0.x; v[1] = p0.y; v[2] = p0.z; v[3] = p0.w;
                 v[4] = p1.x; v[5] = p1.y; v[6] = p1.z; v[7] = p1.w;
             }
-            float lo = v[0], hi = v[0];
-#pragma unroll
-            for (int e = 1; e < 8; e++) { lo = fminf(lo, v[e]); hi = fmaxf(hi, v[e]); }
-            group_minmax<G8>(lo, hi);
-            const GroupParams gp = group_params(lo, hi);
-            const uint32_t word = quant_word8(v, gp);
+            GroupParams gp;
+        const uint32_t word = quant_group8<G8>(v, gp);
             if (ok) {
                 *reinterpret_cast<uint32_t *>(a.codes + orow * (N / 2) + ch * 4) = word;
                 if ((ch % G8) == 0) {

@@ -1,0 +1,43 @@
+// Launchers of the stand-alone kernels: dequantization, the hooks' quantizer
+// (hooks.hip) and the W4A4 GEMM (w4a4.hip).
+#include "host.hpp"
+
+namespace narhip {
+namespace host {
+
+int launch_dequant(const uint8_t *codes, const uint16_t *scales, const uint16_t *zeros, int64_t rows, int64_t n,
+                   int group, float *out, hipStream_t s)
+{
+    const int64_t words = rows * n / 8;
+    hipLaunchKernelGGL(dequant_kernel<>, dim3((unsigned)((words + 255) / 256)), dim3(256), 0, s, codes, scales, zeros,
+                       rows, n, group, out);
+    return check_launch("dequant_kernel");
+}
+
+int launch_quant_tuple(int dtype, const void *x, int64_t elems, int group, uint8_t *codes, uint16_t *scales,
+                       uint16_t *zeros, void *deq, hipStream_t s)
+{
+    dim3 grid((unsigned)((elems / 8 + 255) / 256));
+    switch (dtype) {
+    case DT_F32: hipLaunchKernelGGL(quant_tuple_kernel<DT_F32>, grid, dim3(256), 0, s, x, elems, group, codes, scales, zeros, deq); break;
+    case DT_BF16: hipLaunchKernelGGL(quant_tuple_kernel<DT_BF16>, grid, dim3(256), 0, s, x, elems, group, codes, scales, zeros, deq); break;
+    default: hipLaunchKernelGGL(quant_tuple_kernel<DT_F16>, grid, dim3(256), 0, s, x, elems, group, codes, scales, zeros, deq); break;
+    }
+    return check_launch("quant_tuple_kernel");
+}
+
+// a.out is the output itself (one split) or the fp32 partials [splits][T][O]
+// that the reduction sums in split order into `out`.
+int launch_w4a4(const W4A4Args &a, int64_t gx, int64_t gy, float *out, hipStream_t s)
+{
+    hipLaunchKernelGGL(w4a4_kernel<>, dim3((unsigned)gx, (unsigned)gy, (unsigned)a.splits), dim3(256), 0, s, a);
+    int rc = check_launch("w4a4_kernel");
+    if (rc || a.splits == 1) return rc;
+    const int64_t cnt = a.T * a.O;
+    hipLaunchKernelGGL(w4a4_reduce_kernel<>, dim3((unsigned)((cnt + 255) / 256)), dim3(256), 0, s, a.out, a.splits,
+                       a.T, a.O, out, a.ldo);
+    return check_launch("w4a4_reduce_kernel");
+}
+
+}  // namespace host
+}  // namespace narhip

@@ -267,6 +267,8 @@ __device__ __forceinline__ double row_sum64(double v)
 
 // Min/max over the lanes of a group of G8 chunks (G8 = 4, 8 or 16 lanes, the
 // lanes whose chunk indices share chunk >> log2(G8)).  Exact in any order.
+// fminf/fmaxf drop a NaN operand: the quantizers below use this form on the
+// common path and detect NaN elements from their codes.
 template <int G8>
 __device__ __forceinline__ void group_minmax(float &lo, float &hi)
 {
@@ -276,11 +278,37 @@ __device__ __forceinline__ void group_minmax(float &lo, float &hi)
     if constexpr (G8 >= 16) { lo = fminf(lo, xchg<3>(lo)); hi = fmaxf(hi, xchg<3>(hi)); }
 }
 
+// NaN-propagating min/max, the semantics of torch.amin / torch.amax that the
+// reference's quantizer reduces with (nar/experiment.py:166-167): a NaN
+// operand wins.
+__device__ __forceinline__ float min_nan(float a, float b) { return (b < a || b != b) ? b : a; }
+__device__ __forceinline__ float max_nan(float a, float b) { return (b > a || b != b) ? b : a; }
+
+template <int NV>
+__device__ __forceinline__ void lane_minmax_nan(const float *v, float &lo, float &hi)
+{
+    lo = v[0]; hi = v[0];
+#pragma unroll
+    for (int e = 1; e < NV; e++) { lo = min_nan(lo, v[e]); hi = max_nan(hi, v[e]); }
+}
+
+template <int G8>
+__device__ __forceinline__ void group_minmax_nan(float &lo, float &hi)
+{
+    lo = min_nan(lo, xchg<0>(lo)); hi = max_nan(hi, xchg<0>(hi));
+    lo = min_nan(lo, xchg<1>(lo)); hi = max_nan(hi, xchg<1>(hi));
+    if constexpr (G8 >= 8) { lo = min_nan(lo, xchg<2>(lo)); hi = max_nan(hi, xchg<2>(hi)); }
+    if constexpr (G8 >= 16) { lo = min_nan(lo, xchg<3>(lo)); hi = max_nan(hi, xchg<3>(hi)); }
+}
+
 // ------------------------------------------------------------- quantizer --
 //
 // dynamic_asym_int4 group parameters (nar/experiment.py:166-181):
 //   raw = (hi - lo) / 15 (fp32 division); s16 = fp16(raw > 0 ? raw : 1);
 //   s16 <= 0 -> 1; z16 = fp16(lo).
+// A NaN lo (a group holding a NaN) gives raw = NaN -> s16 = 1 and the
+// canonical quiet NaN 0x7E00 as zero-point, whatever the NaN's sign or payload
+// (torch's min reduction and fp16 conversion return that for +NaN and -NaN).
 struct GroupParams {
     float s, z;
     uint16_t s16, z16;
@@ -293,7 +321,7 @@ __device__ __forceinline__ GroupParams group_params(float lo, float hi)
     float sr = raw > 0.0f ? raw : 1.0f;
     uint16_t sh = f32_to_f16_bits(sr);
     if (!(f16_bits_to_f32(sh) > 0.0f)) sh = 0x3c00u;
-    uint16_t zh = f32_to_f16_bits(lo);
+    uint16_t zh = lo != lo ? (uint16_t)0x7e00u : f32_to_f16_bits(lo);
     g.s16 = sh; g.z16 = zh;
     g.s = f16_bits_to_f32(sh);
     g.z = f16_bits_to_f32(zh);
@@ -301,7 +329,9 @@ __device__ __forceinline__ GroupParams group_params(float lo, float hi)
 }
 
 // q = clamp(round_half_even((x - z) / s), 0, 15) with the fp32 subtraction and
-// the correctly rounded fp32 division of the reference.
+// the correctly rounded fp32 division of the reference.  A NaN quotient
+// (NaN input or zero-point, Inf - Inf, Inf / Inf) gives code 0, the uint8
+// conversion of the reference's NaN.
 __device__ __forceinline__ uint32_t quant_code(float x, const GroupParams &g)
 {
     float d = x - g.z;
@@ -313,30 +343,58 @@ __device__ __forceinline__ uint32_t quant_code(float x, const GroupParams &g)
 // The same code from y = (x - z) * RN(1/s).  y is within 2^-23 |d/s| of the
 // exact quotient and RN(d/s) within 2^-24 |d/s|, so below 16 both round to the
 // same integer unless y lies within 2^-18 of a half-integer; such lanes set
-// `tie` and the caller recomputes with quant_code.  (Half-integers at or above
-// 15.5 and below 0.5 clamp to the same code either way.)
-__device__ __forceinline__ uint32_t quant_code_fast(float x, float z, float rs, bool &tie)
+// `flag` and the caller recomputes with quant_code.  (Half-integers at or above
+// 15.5 and below 0.5 clamp to the same code either way.)  The comparison is
+// written so that a NaN y also sets `flag`: a group holding a NaN element
+// passed the NaN-dropping min/max of the common path, and the caller's slow
+// path recomputes its parameters with the NaN-propagating reduction.
+__device__ __forceinline__ uint32_t quant_code_fast(float x, float z, float rs, bool &flag)
 {
     const float y = (x - z) * rs;
     const float r = __builtin_rintf(y);
-    tie |= __builtin_fabsf(y - r) >= 0.5f - 0x1p-18f;
+    flag |= !(__builtin_fabsf(y - r) < 0.5f - 0x1p-18f);
     return (uint32_t)fminf(fmaxf(r, 0.0f), 15.0f);
 }
 
 // Eight codes of one lane packed into a 32-bit word (nibble e = element e).
-// Bit-identical to eight quant_code calls; the exact division only runs for
-// waves that hold a near-tie.
-__device__ __forceinline__ uint32_t quant_word8(const float *v, const GroupParams &g)
+__device__ __forceinline__ uint32_t quant_word8_exact(const float *v, const GroupParams &g)
 {
-    const float rs = 1.0f / g.s;
-    bool tie = false;
     uint32_t word = 0;
 #pragma unroll
-    for (int e = 0; e < 8; e++) word |= quant_code_fast(v[e], g.z, rs, tie) << (4 * e);
-    if (__builtin_expect(__any(tie), 0)) {
-        word = 0;
+    for (int e = 0; e < 8; e++) word |= quant_code(v[e], g) << (4 * e);
+    return word;
+}
+
+__device__ __forceinline__ uint32_t quant_word8_fast(const float *v, const GroupParams &g, bool &flag)
+{
+    const float rs = 1.0f / g.s;
+    uint32_t word = 0;
 #pragma unroll
-        for (int e = 0; e < 8; e++) word |= quant_code(v[e], g) << (4 * e);
+    for (int e = 0; e < 8; e++) word |= quant_code_fast(v[e], g.z, rs, flag) << (4 * e);
+    return word;
+}
+
+// One lane's 8 values of a group that spans G8 lanes of a row (group_minmax):
+// the group parameters in g and the lane's packed codes.  Bit-identical to the
+// reference quantizer: the common path reduces with fminf/fmaxf and takes the
+// codes from the reciprocal; a wave holding a near-tie or a NaN element redoes
+// the reduction with NaN propagation, the parameters and the exact codes.
+// Every lane of the wave must call it (cross-lane moves, wave-uniform branch).
+template <int G8>
+__device__ __forceinline__ uint32_t quant_group8(const float *v, GroupParams &g)
+{
+    float lo = v[0], hi = v[0];
+#pragma unroll
+    for (int e = 1; e < 8; e++) { lo = fminf(lo, v[e]); hi = fmaxf(hi, v[e]); }
+    group_minmax<G8>(lo, hi);
+    g = group_params(lo, hi);
+    bool flag = false;
+    uint32_t word = quant_word8_fast(v, g, flag);
+    if (__builtin_expect(__any(flag), 0)) {
+        lane_minmax_nan<8>(v, lo, hi);
+        group_minmax_nan<G8>(lo, hi);
+        g = group_params(lo, hi);
+        word = quant_word8_exact(v, g);
     }
     return word;
 }

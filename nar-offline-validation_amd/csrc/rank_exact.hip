@@ -8,6 +8,7 @@
 // partial[t, s*k + r]) computed as the exact sums: every product of a bf16 or
 // fp32 value with an fp32 factor is exact in fp64, each thread adds its
 // channels in index order.  Tiles of 32 tokens share every factor read.
+#pragma once
 #include "narhip_device.hpp"
 
 namespace narhip {
@@ -22,6 +23,7 @@ struct ProjArgs {
 };
 
 // grid: (ceil(T/32), splits); block 256.  Thread (tt, r) pairs are strided.
+template <int = 0>
 __global__ void __launch_bounds__(256)
 proj_exact_kernel(ProjArgs a)
 {
@@ -173,6 +175,7 @@ proj_f64_kernel(ProjF64Args a)
 }
 
 // u[t, r] = RN32( sum_s pd[t][s][r] ), fp64 partials folded in split order.
+template <int = 0>
 __global__ void __launch_bounds__(256)
 fold_f64_kernel(const double *pd, int splits, int kmax, int k, int64_t T, float *u)
 {
@@ -188,6 +191,7 @@ fold_f64_kernel(const double *pd, int splits, int kmax, int k, int64_t T, float 
 
 // u[t, r] = RN32( sum_s partial[t, s*k + r] ), the split partials folded in
 // fp64 in split order (one thread per (t, r)).
+template <int = 0>
 __global__ void __launch_bounds__(256)
 fold_f32_kernel(const float *partial, int splits, int k, int64_t T, float *u)
 {
@@ -210,6 +214,7 @@ struct CorrArgs {
 };
 
 // grid: (ceil(T/32), n/64); block 256: thread = (token tt = tid/8, 8 columns).
+template <int = 0>
 __global__ void __launch_bounds__(256)
 corr_exact_kernel(CorrArgs a)
 {

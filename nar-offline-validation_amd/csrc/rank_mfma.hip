@@ -12,12 +12,14 @@
 //   corr_quant      : x' = P - u W^T with u and W^T both as three bf16 terms
 //                     (the six term products of weight >= 2^-16), then the
 //                     INT4 quantizer of nar/experiment.py:158-184
+#pragma once
 #include "mfma.hpp"
 #include "narhip_device.hpp"
 
 namespace narhip {
 
 // v [n, k] fp32 -> vt [3][kp16][n] bf16 (rank-major, zero rows for r >= k)
+template <int = 0>
 __global__ void __launch_bounds__(256)
 prep_v_kernel(const float *v, int64_t n, int k, int kp, __bf16 *vt)
 {
@@ -34,6 +36,7 @@ prep_v_kernel(const float *v, int64_t n, int k, int kp, __bf16 *vt)
 }
 
 // w_t [k, n] fp32 -> wtt [3][n][kp32] bf16 (channel-major, zero ranks for r >= k)
+template <int = 0>
 __global__ void __launch_bounds__(256)
 prep_w_kernel(const float *wt, int64_t n, int k, int kp, __bf16 *wtt)
 {
@@ -191,6 +194,7 @@ proj_mfma_kernel(ProjMfmaArgs a)
 
 // u for each token from the split partials: fp64 fold in split order, rounded
 // once to fp32, then split in three bf16 terms.  u3 [T][3][kp] (zero for r >= k).
+template <int = 0>
 __global__ void __launch_bounds__(256)
 fold_u_kernel(const float *partial, int splits, int k, int kp, int64_t T, __bf16 *u3)
 {
@@ -298,17 +302,22 @@ __device__ __forceinline__ void cq_group(CqUnit<B> (&xt)[2], const CorrQuantArgs
             for (int i = 0; i < 4; i++) { lo = fminf(lo, xv[mt][i]); hi = fmaxf(hi, xv[mt][i]); }
         lo = fminf(lo, __shfl_xor(lo, 16)); hi = fmaxf(hi, __shfl_xor(hi, 16));
         lo = fminf(lo, __shfl_xor(lo, 32)); hi = fmaxf(hi, __shfl_xor(hi, 32));
-        const GroupParams gp = group_params(lo, hi);
+        GroupParams gp = group_params(lo, hi);
         const float rs = 1.0f / gp.s;
-        bool tie = false;
+        bool flag = false;
         uint32_t q16[MTG];
 #pragma unroll
         for (int mt = 0; mt < MTG; mt++) {
             q16[mt] = 0;
 #pragma unroll
-            for (int i = 0; i < 4; i++) q16[mt] |= quant_code_fast(xv[mt][i], gp.z, rs, tie) << (4 * i);
+            for (int i = 0; i < 4; i++) q16[mt] |= quant_code_fast(xv[mt][i], gp.z, rs, flag) << (4 * i);
         }
-        if (__builtin_expect(__any(tie), 0)) {
+        if (__builtin_expect(__any(flag), 0)) {
+            // a near-tie or a NaN element: NaN-propagating parameters, exact codes
+            lane_minmax_nan<4 * MTG>(&xv[0][0], lo, hi);
+            lo = min_nan(lo, __shfl_xor(lo, 16)); hi = max_nan(hi, __shfl_xor(hi, 16));
+            lo = min_nan(lo, __shfl_xor(lo, 32)); hi = max_nan(hi, __shfl_xor(hi, 32));
+            gp = group_params(lo, hi);
 #pragma unroll
             for (int mt = 0; mt < MTG; mt++) {
                 q16[mt] = 0;
@@ -439,6 +448,7 @@ corr_quant_kernel(CorrQuantArgs a)
 }
 
 // Device self-test of the operand mapping: one MFMA on per-lane inputs.
+template <int = 0>
 __global__ void mfma_probe_kernel(const __bf16 *a, const __bf16 *b, float *d)
 {
     const int l = threadIdx.x;

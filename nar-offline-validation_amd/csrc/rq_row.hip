@@ -10,6 +10,7 @@
 // staged in LDS, the Paley product reads one column of F per thread.  The
 // Paley sum is accumulated in fp64 in index order and rounded once -- the
 // definition the oracle uses for the reference's BLAS product.
+#pragma once
 #include "narhip_device.hpp"
 
 namespace narhip {
@@ -153,12 +154,8 @@ rq_row_kernel(RowArgs a)
             v[0] = p0.x; v[1] = p0.y; v[2] = p0.z; v[3] = p0.w;
             v[4] = p1.x; v[5] = p1.y; v[6] = p1.z; v[7] = p1.w;
         }
-        float lo = v[0], hi = v[0];
-#pragma unroll
-        for (int e = 1; e < 8; e++) { lo = fminf(lo, v[e]); hi = fmaxf(hi, v[e]); }
-        group_minmax<G8>(lo, hi);
-        const GroupParams g = group_params(lo, hi);
-        const uint32_t word = quant_word8(v, g);
+        GroupParams g;
+        const uint32_t word = quant_group8<G8>(v, g);
         if (ok) {
             *reinterpret_cast<uint32_t *>(a.codes + orow * (N / 2) + ch * 4) = word;
             if ((ch % G8) == 0) {

@@ -10,6 +10,7 @@
 // Stages w = 1,2,4 are in-register, w = 8..64 are DPP exchanges inside the row,
 // w = 128.. are in-register again -- the reference's stage order
 // (nar/extended_experiment.py:443-456) is preserved exactly.
+#pragma once
 #include "narhip_device.hpp"
 
 namespace narhip {
@@ -173,12 +174,8 @@ rq_seg_kernel(SegArgs a)
     const int64_t gpt = a.n / B;   // groups per token
 #pragma unroll
     for (int h = 0; h < NH; h++) {
-        float lo = v[h * 8], hi = v[h * 8];
-#pragma unroll
-        for (int e = 1; e < 8; e++) { lo = fminf(lo, v[h * 8 + e]); hi = fmaxf(hi, v[h * 8 + e]); }
-        group_minmax<G8>(lo, hi);
-        const GroupParams g = group_params(lo, hi);
-        const uint32_t word = quant_word8(v + h * 8, g);
+        GroupParams g;
+        const uint32_t word = quant_group8<G8>(v + h * 8, g);
         if (active) {
             const int64_t pos = base + h * 128 + chunk * 8;
             *reinterpret_cast<uint32_t *>(a.codes + orow * (a.n / 2) + pos / 2) = word;

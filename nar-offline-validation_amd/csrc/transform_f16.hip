@@ -25,6 +25,7 @@
 //                     butterflies, the division and the fp64 correction sum are
 //                     those of the segment kernel, so the fp32 values equal its;
 //                     then fp16 out, or (QUANT) the group-128 INT4 quantizer.
+#pragma once
 #include "narhip_device.hpp"
 
 namespace narhip {
@@ -289,12 +290,8 @@ __device__ __forceinline__ void xform_token(const XformArgs &a, const double (&W
     for (int e = 0; e < 8; e++) v[e] = v[e] - (float)acc[e];
     if constexpr (QUANT) {
         // the segment is one group of 128: min/max over the row, then the codes
-        float lo = v[0], hi = v[0];
-#pragma unroll
-        for (int e = 1; e < 8; e++) { lo = fminf(lo, v[e]); hi = fmaxf(hi, v[e]); }
-        group_minmax<16>(lo, hi);
-        const GroupParams g = group_params(lo, hi);
-        const uint32_t word = quant_word8(v, g);
+        GroupParams g;
+        const uint32_t word = quant_group8<16>(v, g);
         if (active) {
             const int64_t orow = a.dest ? a.dest[t] : t;
             *reinterpret_cast<uint32_t *>(a.codes + orow * (a.n / 2) + ch / 2) = word;

@@ -25,6 +25,7 @@
 // buffers, one barrier per group).  Dispatch is round-robin over the 8 XCDs by
 // linear block id, so when gridDim.x (weight tiles) is a multiple of 8 all
 // blocks of one weight tile run on one XCD and share its L2.
+#pragma once
 #include "narhip_device.hpp"
 
 namespace narhip {
@@ -88,6 +89,7 @@ __device__ __forceinline__ uint32_t wq_unpack(const WqStage &st, uint8_t *dst)
     return sum;
 }
 
+template <int = 0>
 __global__ void __launch_bounds__(256, 2)
 w4a4_kernel(W4A4Args a)
 {
@@ -215,6 +217,7 @@ w4a4_kernel(W4A4Args a)
 }
 
 // out[t, o] = sum over splits s, in order, of part[s][t][o].
+template <int = 0>
 __global__ void __launch_bounds__(256)
 w4a4_reduce_kernel(const float *part, int splits, int64_t T, int64_t O, float *out, int64_t ldo)
 {

@@ -315,8 +315,10 @@ int nar_oracle_quant(const float *xr, int64_t T, int64_t n, int64_t ldx, int b,
                     else *dst = (uint8_t)(*dst | (c << 4));
                 }
                 if (deq) {
+                    /* the reference dequantizes the clamped float quotient: a NaN
+                     * quotient (x - z = Inf - Inf, or Inf / Inf) stays NaN */
                     float prod = (float)c * s;
-                    deq[idx] = prod + z;
+                    deq[idx] = isnan(qf) ? qf : prod + z;
                 }
             }
         }

@@ -64,6 +64,10 @@ def _rq(lib, **kw):
     (dict(m=28, q=512, n=14336, ld=14336, k=32, nb=14336, v=16, wt=16, x=16, codes=16, scales=16, zeros=16), -4),
     (dict(m=28, q=512, n=14336, ld=14336, k=32, nb=14336), -1),   # rank factors missing
     (dict(ld=1000), -1),
+    # prepared terms do not stand in for w_t on the paths that read w_t itself
+    (dict(k=8, v=16, prepared=16, x=16, codes=16, scales=16, zeros=16), -1),              # k < 16, AUTO
+    (dict(m=28, q=512, n=14336, ld=14336, k=32, nb=14336, v=16, prepared=16, x=16, codes=16, scales=16,
+          zeros=16, mode=1), -1),                                                          # RANK_EXACT
 ])
 def test_host_validation(kw, code):
     import narhip
@@ -137,3 +141,14 @@ def test_rank_projection_f16_host_validation(k, n, splits, code):
     ld = (n + 7) // 8 * 8
     assert lib.narhip_rank_projection_f16(None, 4, n, ld, None, k, splits, None, None) == code
     assert lib.narhip_last_error_string() != b""
+
+
+def test_group_quant_requires_w_t_off_the_mfma_path():
+    """Kernel B with prepared terms but no w_t: only the MFMA rank path may go on."""
+    import narhip
+    lib = narhip.load()
+    args = [16, 4, 1024, 1024, 1, 128, 16, 1, 8, None, 16, 128, 16, 16, 16, 0, None, 0, None]
+    assert lib.narhip_group_quant(*args) == -1
+    assert b"w_t" in lib.narhip_last_error_string()
+    exact = [16, 4, 14336, 14336, 28, 512, 16, 1, 32, None, 16, 128, 16, 16, 16, 1, None, 0, None]
+    assert lib.narhip_group_quant(*exact) == -1

@@ -259,3 +259,36 @@ def test_comparator_classifies_ties():
     gross = O.quant(x * np.float32(1.001), 128)
     rep2 = O.compare_quant(x, ref, gross.codes, gross.scales, gross.zeros, 128, rel_err=2.0 ** -22)
     assert not rep2.within_contract()
+
+
+def test_quantizer_nonfinite_groups_match_reference():
+    """Groups holding NaN or +-Inf (tests/golden/make_nonfinite_vectors.py, written
+    from nar/experiment.py:dynamic_asym_int4): NaN wins the group min/max
+    (torch.amin/amax), the zero-point is the canonical quiet NaN, codes of NaN
+    quotients are 0 and their dequantized values NaN."""
+    nf = np.load(GOLD / "nonfinite_vectors.npz")
+    names = list(nf["nf_names"])
+    assert len(names) >= 27
+    for key in names:
+        x = nf[key + "_x"]
+        b = int(key.split("_b")[-1])
+        with np.errstate(invalid="ignore", over="ignore"):
+            r = O.quant(x, b)
+        assert np.array_equal(r.codes, nf[key + "_codes"]), key
+        assert np.array_equal(r.scales, nf[key + "_scale"]), key
+        assert np.array_equal(r.zeros, nf[key + "_zero"]), key
+        assert np.array_equal(r.deq, nf[key + "_deq"], equal_nan=True), key
+
+
+def test_quantizer_nonfinite_planted_mistake_fails():
+    """Dequantizing the integer code (0 * 1 + Inf = Inf) instead of the NaN
+    quotient must disagree with the reference on an all-Inf group."""
+    nf = np.load(GOLD / "nonfinite_vectors.npz")
+    key = "nf_all_inf_b32"
+    r = O.quant(nf[key + "_x"], 32)
+    codes = r.codes.astype(np.float32).reshape(r.deq.shape)
+    s = O.f16_bits_to_f32(r.scales).repeat(32, axis=1)
+    z = O.f16_bits_to_f32(r.zeros).repeat(32, axis=1)
+    with np.errstate(invalid="ignore"):
+        wrong = codes * s + z
+    assert not np.array_equal(wrong, nf[key + "_deq"], equal_nan=True)
