@@ -102,7 +102,23 @@ def test_rotate_quant_nonfinite_rows(path, value):
         rot = O.rotate(O.bf16_to_f32(bits), m, q, v=w.v, wt=w.w_t, rank_block=w.rank_block)
         ref = O.quant(rot, w.group)
     c, s, z = codes.cpu().numpy(), f16_bits(scales), f16_bits(zeros)
-    bad_rows = np.nonzero((c != ref.packed).any(1) | (s != ref.scales).any(1) | (z != ref.zeros).any(1))[0]
-    assert bad_rows.size == 0, f"rows {bad_rows.tolist()} differ"
+    planted_rows = np.arange(0, w.tokens, 2)
+    other_rows = np.arange(1, w.tokens, 2)
+    bad = (c != ref.packed).any(1) | (s != ref.scales).any(1) | (z != ref.zeros).any(1)
+    for r in np.nonzero(bad)[0]:
+        print(f"   row {r}: codes {(c[r] != ref.packed[r]).sum()} scales {(s[r] != ref.scales[r]).sum()} "
+              f"zeros {(z[r] != ref.zeros[r]).sum()}", flush=True)
+    # the rows holding a non-finite input: bit for bit on every path
+    assert not bad[planted_rows].any(), f"planted rows {np.nonzero(bad)[0].tolist()} differ"
+    if path.startswith("kron_mfma"):
+        # finite rows of the MFMA rank path: the tie contract of that path
+        sub = O.Quantized(*(getattr(ref, f)[other_rows] for f in ("codes", "packed", "scales", "zeros", "deq")))
+        rep = O.compare_quant(rot[other_rows], sub, O.unpack(c[other_rows], w.n), s[other_rows], z[other_rows],
+                              w.group, rel_err=2.0 ** -21)
+        print("  ", rep, flush=True)
+        assert rep.code_max_abs_diff <= 1 and rep.code_mismatch_unexplained == 0
+        assert rep.scale_mismatch_unexplained == 0 and rep.zero_mismatch_unexplained == 0
+    else:
+        assert not bad.any(), f"rows {np.nonzero(bad)[0].tolist()} differ"
     # the planted rows really are non-finite after the transform
     assert (~np.isfinite(rot[0])).any()
