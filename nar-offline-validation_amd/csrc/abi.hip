@@ -314,10 +314,10 @@ int run_rotate_quant(const void *x_bf16, int64_t T, int64_t n, int64_t ldx, int 
             }
             CorrQuantArgs ca{};
             ca.P = Pbuf; ca.T = tn; ca.n = n; ca.u3 = u3;
-            ca.dummy = reinterpret_cast<uint8_t *>(u3) + align256(u3_bytes(tn, k));
             ca.wtt = reinterpret_cast<const __bf16 *>(static_cast<const char *>(prep) + vt_bytes(n, k));
             ca.kp = kp32(k);
             ca.dest = dest ? dest + t0 : nullptr;
+            ca.dummy = reinterpret_cast<uint8_t *>(u3) + align256(u3_bytes(tn, k));
             const int64_t row0 = dest ? 0 : t0;
             ca.codes = codes + row0 * (n / 2);
             ca.scales = static_cast<uint16_t *>(scales) + row0 * (n / group);

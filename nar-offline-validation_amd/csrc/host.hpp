@@ -7,6 +7,7 @@
 #pragma once
 
 #include "../../include/narhip.h"
+#include "corr_quant.hip"
 #include "dequant.hip"
 #include "hooks.hip"
 #include "kron_mfma.hip"
@@ -103,12 +104,13 @@ inline int mfma_splits(int64_t T, int64_t n)
 }
 inline bool mfma_projection_ok(int64_t n, int splits) { return n % (128 * (int64_t)splits) == 0; }
 
-// u terms [T][3][kp32] bf16, then a scratch row of n/2 bytes for the stores of
-// out-of-range tokens of the last tile (n/2 + 4 KB: codes, scales, rotated x')
+// u terms [T][3][kp32] bf16 (the MFMA correction's B operand), then the
+// correction kernel's scratch area for the stores of lanes with nothing to store
 inline size_t u3_bytes(int64_t T, int k) { return sizeof(uint16_t) * 3 * (size_t)kp32(k) * (size_t)T; }
 inline size_t corr_scratch_bytes(int64_t T, int64_t n, int k)
 {
-    return align256(u3_bytes(T, k)) + align256((size_t)n / 2 + 4096);
+    (void)n;
+    return align256(u3_bytes(T, k)) + CQ_DUMMY_BYTES;
 }
 
 // fp16 transform at q = 128, k <= 8: proj_tok (unless the caller brings

@@ -99,47 +99,44 @@ int launch_fold_u(const float *partial, int splits, int k, int kp, int64_t T, __
 
 namespace {
 
-template <int B, int KS, int CW>
+template <int B, int KS, int TPW>
 int launch_cq(const CorrQuantArgs &a, dim3 grid, hipStream_t s)
 {
-    if (a.rotated) hipLaunchKernelGGL((corr_quant_kernel<B, KS, CW, true>), grid, dim3(256), 0, s, a);
-    else hipLaunchKernelGGL((corr_quant_kernel<B, KS, CW, false>), grid, dim3(256), 0, s, a);
+    if (a.rotated) hipLaunchKernelGGL((corr_quant_kernel<B, KS, true, TPW>), grid, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((corr_quant_kernel<B, KS, false, TPW>), grid, dim3(256), 0, s, a);
     return check_launch("corr_quant_kernel");
 }
 
-template <int B>
-int launch_cq_b(const CorrQuantArgs &a, int ks, int cw, dim3 grid, hipStream_t s)
+template <int B, int KS>
+int launch_cq_t(const CorrQuantArgs &a, dim3 grid, hipStream_t s)
 {
-    if (ks == 1 && cw == 256) return launch_cq<B, 1, 256>(a, grid, s);
-    if (ks == 1) return launch_cq<B, 1, 128>(a, grid, s);
-    return launch_cq<B, 2, 128>(a, grid, s);
+    return a.tpg == 16 ? launch_cq<B, KS, 4>(a, grid, s) : launch_cq<B, KS, 1>(a, grid, s);
 }
 
 }  // namespace
 
-// Workgroups own 48 KB of W^T terms (256 channels at k <= 32, else 128) and
-// run enough 128-token tiles over them that about 1024 workgroups remain.
+// A workgroup owns one 128-channel block and tpg 16-token tiles (tpg / 4 per
+// wave): 16 tiles where that still leaves about 2048 workgroups or more, else 4.
 int launch_corr_quant(CorrQuantArgs a, int b, hipStream_t s)
 {
     if (a.T == 0) return NARHIP_OK;
+    if (a.n % CQ_CB) return fail(NARHIP_EUNSUPPORTED, "rank correction needs n %% 128 == 0");
     const int ks = a.kp / 32;
-    // 256 channels (48 KB of W^T terms) per workgroup where the register tile
-    // of two groups fits (b <= 64, k <= 32); else one 128-channel block
-    const int cw = (ks == 1 && b <= 64 && a.n % 256 == 0) ? 256 : 128;
-    if (a.n % cw || cw % b) return fail(NARHIP_EUNSUPPORTED, "rank correction needs n %% 128 == 0");
-    a.ncb = a.n / cw;
-    const int64_t tiles = (a.T + 127) / 128;
-    int tpw = 1;
-    while (tpw < 8 && a.ncb * ((tiles + 2 * tpw - 1) / (2 * tpw)) >= 1024) tpw *= 2;
-    a.tpw = tpw;
-    const int64_t groups = (tiles + tpw - 1) / tpw;
+    if (ks < 1 || ks > 2) return fail(NARHIP_EUNSUPPORTED, "rank correction supports k <= 64");
+    a.ncb = a.n / CQ_CB;
+    const int64_t tiles = (a.T + 15) / 16;
+    a.tpg = tiles * a.ncb >= 16 * 2048 ? 16 : 4;
+    const int64_t groups = (tiles + a.tpg - 1) / a.tpg;
     const int64_t blocks = 8 * a.ncb * ((groups + 7) / 8);
     if (blocks > 0x7fffffff) return fail(NARHIP_EUNSUPPORTED, "too many tokens");
-    dim3 grid((unsigned)blocks);
-    switch (b) {
-    case 32: return launch_cq_b<32>(a, ks, cw, grid, s);
-    case 64: return launch_cq_b<64>(a, ks, cw, grid, s);
-    case 128: return launch_cq_b<128>(a, ks, cw, grid, s);
+    const dim3 grid((unsigned)blocks);
+    switch (b * 4 + ks) {
+    case 32 * 4 + 1: return launch_cq_t<32, 1>(a, grid, s);
+    case 32 * 4 + 2: return launch_cq_t<32, 2>(a, grid, s);
+    case 64 * 4 + 1: return launch_cq_t<64, 1>(a, grid, s);
+    case 64 * 4 + 2: return launch_cq_t<64, 2>(a, grid, s);
+    case 128 * 4 + 1: return launch_cq_t<128, 1>(a, grid, s);
+    case 128 * 4 + 2: return launch_cq_t<128, 2>(a, grid, s);
     }
     return fail(NARHIP_EUNSUPPORTED, "group %d not built", b);
 }

@@ -314,10 +314,36 @@ struct GroupParams {
     uint16_t s16, z16;
 };
 
+// RN(d / 15) for d = hi - lo >= 0 (and +Inf, NaN) without a divide:
+// q0 = d * RN(1/15), one Markstein correction q1 = fma(fma(-q0, 15, d), RN(1/15), q0)
+// (Markstein, "Computation of elementary functions on the IBM RISC System/6000
+// processor", IBM J. Res. Dev. 34(1), 1990), +Inf passed through.  Checked
+// against the correctly rounded quotient for every non-negative fp32 pattern
+// (tests/native/group_params_check.c): equal, or both below 2^-25 (fp16 zero).
+__device__ __forceinline__ float div15(float d)
+{
+    constexpr float c = 0x1.111112p-4f;            // RN(1/15)
+    const float q0 = d * c;
+    const float r = __builtin_fmaf(-q0, 15.0f, d);
+    const float q1 = __builtin_fmaf(r, c, q0);
+    return d == __builtin_inff() ? d : q1;
+}
+
+// RN(1/s) for a positive fp16 scale s: one Newton step from the hardware
+// reciprocal (within one ulp), equal to RN(1/s) for every fp16 s
+// (tests/native/group_params_check.c).  s = +Inf gives NaN, which sends every
+// code of its group to the exact path.
+__device__ __forceinline__ float recip_scale(float s)
+{
+    const float r0 = __builtin_amdgcn_rcpf(s);
+    const float e = __builtin_fmaf(-s, r0, 1.0f);
+    return __builtin_fmaf(e, r0, r0);
+}
+
 __device__ __forceinline__ GroupParams group_params(float lo, float hi)
 {
     GroupParams g;
-    float raw = (hi - lo) / 15.0f;
+    float raw = div15(hi - lo);
     float sr = raw > 0.0f ? raw : 1.0f;
     uint16_t sh = f32_to_f16_bits(sr);
     if (!(f16_bits_to_f32(sh) > 0.0f)) sh = 0x3c00u;
@@ -367,7 +393,7 @@ __device__ __forceinline__ uint32_t quant_word8_exact(const float *v, const Grou
 
 __device__ __forceinline__ uint32_t quant_word8_fast(const float *v, const GroupParams &g, bool &flag)
 {
-    const float rs = 1.0f / g.s;
+    const float rs = recip_scale(g.s);
     uint32_t word = 0;
 #pragma unroll
     for (int e = 0; e < 8; e++) word |= quant_code_fast(v[e], g.z, rs, flag) << (4 * e);

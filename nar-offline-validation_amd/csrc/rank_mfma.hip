@@ -9,9 +9,7 @@
 //                     accumulators, folded in fp64 at the end of the split
 //   fold_u          : u = fp64 fold of the split partials, rounded once, as
 //                     three bf16 terms per token
-//   corr_quant      : x' = P - u W^T with u and W^T both as three bf16 terms
-//                     (the six term products of weight >= 2^-16), then the
-//                     INT4 quantizer of nar/experiment.py:158-184
+//   (the correction and quantizer that consume u are in corr_quant.hip)
 #pragma once
 #include "mfma.hpp"
 #include "narhip_device.hpp"
@@ -211,240 +209,6 @@ fold_u_kernel(const float *partial, int splits, int k, int kp, int64_t T, __bf16
     split3((float)sum, h, m, l);
     __bf16 *o = u3 + t * 3 * kp + r;
     o[0] = h; o[kp] = m; o[2 * kp] = l;
-}
-
-struct CorrQuantArgs {
-    const float *P;        // [T, n] rotated rows before the rank term
-    int64_t T, n;
-    const __bf16 *u3;      // [T][3][kp] terms of u
-    const __bf16 *wtt;     // [3][n][kp] terms of W^T
-    int kp;
-    uint8_t *codes;
-    uint16_t *scales;
-    uint16_t *zeros;
-    const int64_t *dest;
-    float *rotated;        // x' [T, n] (kernel variant ROT only)
-    uint8_t *dummy;        // scratch row (>= n/2 bytes) that takes the stores of tokens >= T
-    int64_t ncb;           // n / CW channel blocks
-    int tpw;               // 128-token tiles per workgroup
-};
-
-// One unit of corr_quant work: 16 tokens (one MFMA N tile) x one quantization
-// group of B channels (B/16 M tiles).  Lane l holds P / x' for token l%16 of
-// the tile and channels 16 mt + 4g .. +3 (g = l/16): B/16 float4 per lane.
-template <int B>
-struct CqUnit {
-    float v[B / 16][4];
-};
-
-template <int B>
-__device__ __forceinline__ void cq_load(CqUnit<B> &p, const float *prow)
-{
-#pragma unroll
-    for (int mt = 0; mt < B / 16; mt++) {
-        const float4 pv = *reinterpret_cast<const float4 *>(prow + 16 * mt);
-        p.v[mt][0] = pv.x; p.v[mt][1] = pv.y; p.v[mt][2] = pv.z; p.v[mt][3] = pv.w;
-    }
-}
-
-// x' = P - u W^T for one group of B channels and both 16-token halves (W^T
-// terms of the group at wl in LDS: rows of WROW bf16, planes of WPLANE; each
-// fragment read once and used for both halves), then codes, scales and zeros
-// staged in LDS: codes of token 16h + c16 at crow[(16h + c16) * CSTRIDE + ...]
-// (uint16 = four codes), scale and zero at sz[2 (16h + c16)], sz[... + 1].
-// Only x' (variant ROT) goes to memory here.
-template <int B, int KS, int WROW, int WPLANE, int CSTRIDE, bool ROT>
-__device__ __forceinline__ void cq_group(CqUnit<B> (&xt)[2], const CorrQuantArgs &a,
-                                         const bf16x8 (&ub)[2][3][KS], float *const (&rrow)[2],
-                                         const __bf16 *wl, uint16_t *crow, uint16_t *sz, int lane)
-{
-    constexpr int MTG = B / 16;
-    const int g = lane >> 4, c16 = lane & 15;
-#pragma unroll
-    for (int mt = 0; mt < MTG; mt++) {
-        const __bf16 *wrow = wl + (16 * mt + c16) * WROW + 8 * g;
-        bf16x8 wh[KS], wm[KS], wo[KS];
-#pragma unroll
-        for (int ks = 0; ks < KS; ks++) {
-            wh[ks] = *reinterpret_cast<const bf16x8 *>(wrow + 32 * ks);
-            wm[ks] = *reinterpret_cast<const bf16x8 *>(wrow + WPLANE + 32 * ks);
-            wo[ks] = *reinterpret_cast<const bf16x8 *>(wrow + 2 * WPLANE + 32 * ks);
-        }
-#pragma unroll
-        for (int h = 0; h < 2; h++) {
-            floatx4 main = zero4(), small = zero4();
-#pragma unroll
-            for (int ks = 0; ks < KS; ks++) {
-                main = mfma_bf16(wh[ks], ub[h][0][ks], main);
-                small = mfma_bf16(wm[ks], ub[h][0][ks], small);
-                small = mfma_bf16(wh[ks], ub[h][1][ks], small);
-                small = mfma_bf16(wo[ks], ub[h][0][ks], small);
-                small = mfma_bf16(wh[ks], ub[h][2][ks], small);
-                small = mfma_bf16(wm[ks], ub[h][1][ks], small);
-            }
-#pragma unroll
-            for (int i = 0; i < 4; i++) xt[h].v[mt][i] = xt[h].v[mt][i] - (main[i] + small[i]);
-        }
-    }
-#pragma unroll
-    for (int h = 0; h < 2; h++) {
-        auto &xv = xt[h].v;
-        if constexpr (ROT) {
-#pragma unroll
-            for (int mt = 0; mt < MTG; mt++)
-                *reinterpret_cast<float4 *>(rrow[h] + 16 * mt) = make_float4(xv[mt][0], xv[mt][1], xv[mt][2], xv[mt][3]);
-        }
-        // the group of token c16 is spread over lanes c16 + 16g
-        float lo = xv[0][0], hi = lo;
-#pragma unroll
-        for (int mt = 0; mt < MTG; mt++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) { lo = fminf(lo, xv[mt][i]); hi = fmaxf(hi, xv[mt][i]); }
-        lo = fminf(lo, __shfl_xor(lo, 16)); hi = fmaxf(hi, __shfl_xor(hi, 16));
-        lo = fminf(lo, __shfl_xor(lo, 32)); hi = fmaxf(hi, __shfl_xor(hi, 32));
-        GroupParams gp = group_params(lo, hi);
-        const float rs = 1.0f / gp.s;
-        bool flag = false;
-        uint32_t q16[MTG];
-#pragma unroll
-        for (int mt = 0; mt < MTG; mt++) {
-            q16[mt] = 0;
-#pragma unroll
-            for (int i = 0; i < 4; i++) q16[mt] |= quant_code_fast(xv[mt][i], gp.z, rs, flag) << (4 * i);
-        }
-        if (__builtin_expect(__any(flag), 0)) {
-            // a near-tie or a NaN element: NaN-propagating parameters, exact codes
-            lane_minmax_nan<4 * MTG>(&xv[0][0], lo, hi);
-            lo = min_nan(lo, __shfl_xor(lo, 16)); hi = max_nan(hi, __shfl_xor(hi, 16));
-            lo = min_nan(lo, __shfl_xor(lo, 32)); hi = max_nan(hi, __shfl_xor(hi, 32));
-            gp = group_params(lo, hi);
-#pragma unroll
-            for (int mt = 0; mt < MTG; mt++) {
-                q16[mt] = 0;
-#pragma unroll
-                for (int i = 0; i < 4; i++) q16[mt] |= quant_code(xv[mt][i], gp) << (4 * i);
-            }
-        }
-#pragma unroll
-        for (int mt = 0; mt < MTG; mt++) crow[(16 * h + c16) * CSTRIDE + 4 * mt + g] = (uint16_t)q16[mt];
-        if (g == 0) {
-            sz[2 * (16 * h + c16)] = gp.s16;
-            sz[2 * (16 * h + c16) + 1] = gp.z16;
-        }
-    }
-}
-
-// grid (8 * ncb * ceil(token groups / 8)), block 256.  A workgroup owns CW
-// channels: it stages their W^T terms in LDS once ([3][CW][KP], 48 KB) and
-// then runs a.tpw tiles of 128 tokens over them.  Within a tile every wave
-// works alone (no further workgroup barriers) on 32 tokens x CW channels:
-// all of its P (128 VGPRs at CW = 256) is requested at once, then the groups
-// are processed in load order, each waiting only for its own loads.  Codes, scales and zeros are staged in LDS and stored
-// after the last unit; tokens >= T store into a scratch row, so that no
-// memory operation sits under a branch and the wait counts stay exact.
-// Workgroups are dispatched to the 8 XCDs round-robin by block id, so the
-// token group is chosen from (id % 8) and the channel block from the quotient:
-// all channel blocks of a token group run on one XCD, and the 2-byte scale and
-// zero stores of those tokens merge into whole lines in that XCD's L2.
-template <int B, int KS, int CW, bool ROT>
-__global__ void __launch_bounds__(256, 2)
-corr_quant_kernel(CorrQuantArgs a)
-{
-    constexpr int KP = 32 * KS;
-    constexpr int WROW = KP + 8;             // padded channel row: fragment reads hit distinct banks
-    constexpr int WPLANE = CW * WROW;
-    constexpr int NG = CW / B;               // groups per channel block
-    constexpr int CSTRIDE = CW / 4 + 8;      // uint16 per token row of staged codes (16-byte rows, padded
-                                             // so the 16 tokens of a store land in different banks)
-    __shared__ __align__(16) __bf16 ws[3 * WPLANE];
-    __shared__ __align__(16) uint16_t cst[4][32 * CSTRIDE];
-    __shared__ __align__(16) uint16_t szs[4][NG][64];   // [2 t + 0] scale, [2 t + 1] zero of token t
-    const int tid = threadIdx.x;
-    const int lane = tid & 63, w = tid >> 6;
-    const int g = lane >> 4, c16 = lane & 15;
-    const int64_t j = (int64_t)blockIdx.x / 8;
-    const int64_t cb = j % a.ncb;
-    const int64_t tg = (j / a.ncb) * 8 + blockIdx.x % 8;
-    if (tg * a.tpw * 128 >= a.T) return;
-    const int64_t cbeg = cb * CW;
-    const int64_t plane = (int64_t)KP * a.n;
-
-    for (int p = tid; p < 3 * CW * (KP / 8); p += 256) {
-        const int term = p / (CW * (KP / 8)), rem = p % (CW * (KP / 8));
-        const int ch = rem / (KP / 8), k8 = rem % (KP / 8);
-        *reinterpret_cast<bf16x8 *>(&ws[term * WPLANE + ch * WROW + k8 * 8]) =
-            load_bf16x8(a.wtt + term * plane + (cbeg + ch) * KP + k8 * 8);
-    }
-    __syncthreads();
-
-    for (int tt = 0; tt < a.tpw; tt++) {
-        const int64_t t0 = (tg * a.tpw + tt) * 128 + w * 32;
-        if (t0 >= a.T) return;
-        // output rows: code stores (token lane/2), scale stores (token lane, lanes < 32)
-        const int64_t tc = t0 + (lane >> 1), ts = t0 + (lane & 31);
-        int64_t crow_out = tc < a.T ? tc : -1, srow_out = ts < a.T ? ts : -1;
-        if (a.dest) {
-            if (crow_out >= 0) crow_out = a.dest[crow_out];
-            if (srow_out >= 0) srow_out = a.dest[srow_out];
-        }
-        const float *prow[2];
-        float *rrow[2];
-        bf16x8 ub[2][3][KS];
-#pragma unroll
-        for (int h = 0; h < 2; h++) {
-            const int64_t t = t0 + 16 * h + c16;
-            const int64_t tk = t < a.T ? t : a.T - 1;
-            prow[h] = a.P + tk * a.n + cbeg + 4 * g;
-            rrow[h] = ROT ? (t < a.T ? a.rotated + tk * a.n + cbeg + 4 * g
-                                     : reinterpret_cast<float *>(a.dummy) + 4 * g) : nullptr;
-#pragma unroll
-            for (int term = 0; term < 3; term++)
-#pragma unroll
-                for (int ks = 0; ks < KS; ks++)
-                    ub[h][term][ks] = load_bf16x8(a.u3 + (tk * 3 + term) * KP + 32 * ks + 8 * g);
-        }
-        CqUnit<B> U[NG][2];
-#pragma unroll
-        for (int gi = 0; gi < NG; gi++)
-#pragma unroll
-            for (int h = 0; h < 2; h++) cq_load<B>(U[gi][h], prow[h] + gi * B);
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int gi = 0; gi < NG; gi++) {
-            float *const rr[2] = {ROT ? rrow[0] + gi * B : nullptr, ROT ? rrow[1] + gi * B : nullptr};
-            cq_group<B, KS, WROW, WPLANE, CSTRIDE, ROT>(U[gi], a, ub, rr, ws + gi * B * WROW,
-                                                        &cst[w][gi * B / 4], &szs[w][gi][0], lane);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        // codes: two lanes per token, CW/4 bytes each (16-byte pieces)
-        {
-            const int half = lane & 1;
-            uint8_t *base = crow_out >= 0 ? a.codes + crow_out * (a.n / 2) + cbeg / 2 : a.dummy;
-            uint4 *dst = reinterpret_cast<uint4 *>(base + half * (CW / 4));
-            const uint4 *src = reinterpret_cast<const uint4 *>(&cst[w][(lane >> 1) * CSTRIDE + half * (CW / 8)]);
-#pragma unroll
-            for (int q = 0; q < CW / 64; q++) dst[q] = src[q];
-        }
-        // scales and zeros: lanes 0..31 write token lane's NG groups (lanes 32..63 repeat them)
-        {
-            uint16_t *sd = srow_out >= 0 ? a.scales + srow_out * (a.n / B) + cbeg / B
-                                         : reinterpret_cast<uint16_t *>(a.dummy);
-            uint16_t *zd = srow_out >= 0 ? a.zeros + srow_out * (a.n / B) + cbeg / B
-                                         : reinterpret_cast<uint16_t *>(a.dummy);
-            const int tl = lane & 31;
-#pragma unroll
-            for (int q = 0; q < NG; q++) {
-                sd[q] = szs[w][q][2 * tl];
-                zd[q] = szs[w][q][2 * tl + 1];
-            }
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    }
 }
 
 // Device self-test of the operand mapping: one MFMA on per-lane inputs.
