@@ -25,10 +25,9 @@ from __future__ import annotations
 
 import torch
 
-from . import _lib
-from .ops import _p, _stream, hadamard_factors, rotate_quant
+from .ops import _ops, hadamard_factors, rotate_quant
 
-_DTYPE_CODE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
+_DTYPES = (torch.float32, torch.bfloat16, torch.float16)
 
 
 def _group_view_check(n: int, group_size: int) -> None:
@@ -40,22 +39,10 @@ def dynamic_asym_int4(x: torch.Tensor, group_size: int):
     """Fake-quantize with one fp16 scale and fp16 zero per group of the last dimension."""
     if not x.is_cuda:
         raise ValueError("dynamic_asym_int4 (narhip) takes device tensors")
-    if x.dtype not in _DTYPE_CODE:
+    if x.dtype not in _DTYPES:
         raise ValueError(f"unsupported dtype {x.dtype}")
-    n = x.shape[-1]
-    _group_view_check(n, group_size)
-    xc = x.contiguous()
-    rows = xc.numel() // n if n else 0
-    lead = tuple(x.shape[:-1])
-    groups = n // group_size
-    codes = torch.empty(lead + (groups, group_size), dtype=torch.uint8, device=x.device)
-    scales = torch.empty(lead + (groups,), dtype=torch.float16, device=x.device)
-    zeros = torch.empty(lead + (groups,), dtype=torch.float16, device=x.device)
-    deq = torch.empty_like(xc)
-    _lib.check(_lib.load().narhip_dynamic_asym_int4(_p(xc), _DTYPE_CODE[x.dtype], rows, n, group_size,
-                                                    _p(codes), _p(scales), _p(zeros), _p(deq),
-                                                    _stream(x.device)))
-    return deq.view(x.shape), scales, zeros, codes
+    _group_view_check(x.shape[-1], group_size)
+    return _ops.dynamic_asym_int4(x, group_size)
 
 
 def _as_bf16_rows(x: torch.Tensor) -> torch.Tensor:
@@ -87,11 +74,7 @@ def full_hadamard_rows(x: torch.Tensor, signs: torch.Tensor | None) -> torch.Ten
     n = x.shape[-1]
     m, q = hadamard_factors(n)
     xb = _as_bf16_rows(x)
-    out = torch.empty(xb.shape, dtype=torch.float32, device=x.device)
-    s = _signs_f32(signs, n, x.device)
-    _lib.check(_lib.load().narhip_hadamard_rows(_p(xb), xb.shape[0], n, n, m, q, _p(s), _p(out),
-                                                _stream(x.device)))
-    return out.view(x.shape)
+    return _ops.hadamard_rows(xb, m, q, _signs_f32(signs, n, x.device)).view(x.shape)
 
 
 def rotate_dynamic_asym_int4(x: torch.Tensor, group_size: int, *, signs: torch.Tensor | None = None,

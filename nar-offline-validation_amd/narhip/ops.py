@@ -1,9 +1,11 @@
-"""Torch-facing wrappers of the narhip C ABI.
+"""Keyword-friendly wrappers of the narhip operators.
 
-Tensors stay on the GPU and are passed to the library as raw pointers; kernels
-run on the current HIP stream of the tensor's device.  Outputs are allocated
-here when the caller does not pass them (the reference's launchers take them
-preallocated; both forms are supported).
+Each function checks its arguments the way the reference's launchers do
+(``ValueError`` for dtype, device, shape and layout) and then calls the
+registered ``torch.ops.narhip`` operator (narhip/library.py), which runs the
+HIP kernels on the current stream of the tensors' device.  Outputs are
+allocated here when the caller does not pass them (the reference's launchers
+take them preallocated; both forms are supported).
 """
 
 from __future__ import annotations
@@ -14,6 +16,9 @@ import math
 import torch
 
 from . import _lib
+from . import library  # noqa: F401  (registers torch.ops.narhip)
+
+_ops = torch.ops.narhip
 
 RANK_AUTO, RANK_EXACT, RANK_MFMA = _lib.RANK_AUTO, _lib.RANK_EXACT, _lib.RANK_MFMA
 
@@ -55,26 +60,24 @@ def paley(m: int) -> torch.Tensor:
     return out
 
 
-def prepare_rank_factors(v: torch.Tensor | None, w_t: torch.Tensor | None, n: int, k: int,
-                         out: torch.Tensor | None = None) -> torch.Tensor:
+def prepare_rank_factors(v: torch.Tensor | None, w_t: torch.Tensor | None, n: int, k: int) -> torch.Tensor:
     """V and W''^T as exact bf16 term triples in the MFMA layouts (uint8 buffer).
 
     Done once per factor set, like the reference's term padding in
     FoldedR4.from_factor / NARDownTransform.__init__."""
     ref = v if v is not None else w_t
+    if ref is None:
+        raise ValueError("pass v, w_t or both")
     dev = ref.device
     if v is not None:
         _require(v, torch.float32, "v", dev)
+        if tuple(v.shape) != (n, k):
+            raise ValueError(f"v must be [{n}, {k}], got {tuple(v.shape)}")
     if w_t is not None:
         _require(w_t, torch.float32, "w_t", dev)
-    lib = _lib.load()
-    nbytes = lib.narhip_rank_factors_bytes(n, k)
-    if nbytes == 0:
-        raise ValueError(f"no prepared layout for n={n}, k={k}")
-    if out is None:
-        out = torch.empty(nbytes, dtype=torch.uint8, device=dev)
-    _lib.check(lib.narhip_prepare_rank_factors(_p(v), _p(w_t), n, k, _p(out), out.numel(), _stream(dev)))
-    return out
+        if tuple(w_t.shape) != (k, n):
+            raise ValueError(f"w_t must be [{k}, {n}], got {tuple(w_t.shape)}")
+    return _ops.prepare_rank_factors(v, w_t, n, k)
 
 
 def rotate_quant(x: torch.Tensor, *, hadamard: tuple[int, int] = (1, 128),
@@ -117,12 +120,18 @@ def rotate_quant(x: torch.Tensor, *, hadamard: tuple[int, int] = (1, 128),
             raise ValueError(f"w_t must be [{k}, {n}], got {tuple(w_t.shape)}")
     if signs is not None:
         _require(signs, torch.float32, "signs", dev)
-    splits = 0
     if partial is not None:
         _require(partial, torch.float32, "partial", dev)
         if not k or partial.shape[0] != T or partial.shape[1] % k:
             raise ValueError("partial must be [tokens, splits*k]")
-        splits = partial.shape[1] // k
+    nb = n if rank_block is None else int(rank_block)
+    if rotated is not None:
+        _require(rotated, torch.float32, "rotated", dev)
+    if dest_rows is not None:
+        _require(dest_rows, torch.int64, "dest_rows", dev)
+    if codes is None and scales is None and zeros is None and rotated is None and dest_rows is None \
+            and out_rows is None:
+        return _ops.rotate_quant(x, m, q, signs, v, w_t, prepared, nb, partial, group, rank_mode)
     rows = T if out_rows is None else out_rows
     if codes is None:
         codes = torch.empty((rows, n // 2), dtype=torch.uint8, device=dev)
@@ -133,20 +142,8 @@ def rotate_quant(x: torch.Tensor, *, hadamard: tuple[int, int] = (1, 128),
     for t, name, dt in ((codes, "codes", torch.uint8), (scales, "scales", torch.float16),
                         (zeros, "zeros", torch.float16)):
         _require(t, dt, name, dev)
-    if rotated is not None:
-        _require(rotated, torch.float32, "rotated", dev)
-    if dest_rows is not None:
-        _require(dest_rows, torch.int64, "dest_rows", dev)
-    nb = n if rank_block is None else int(rank_block)
-    lib = _lib.load()
-    ws_bytes = lib.narhip_rotate_quant_workspace(T, n, m, q, k, nb, int(partial is not None), splits,
-                                                 int(prepared is not None), rank_mode)
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
-    rc = lib.narhip_rotate_quant(
-        _p(x), T, n, x.stride(0), m, q, _p(signs), k, nb, _p(v), _p(w_t), _p(prepared), _p(partial), splits,
-        group, _p(codes), _p(scales), _p(zeros), _p(rotated), _p(dest_rows), rank_mode,
-        _p(ws), ws_bytes, _stream(dev))
-    _lib.check(rc)
+    _ops.rotate_quant_out(x, m, q, signs, v, w_t, prepared, nb, partial, group, dest_rows, rank_mode,
+                          codes, scales, zeros, rotated)
     return codes, scales, zeros
 
 
@@ -166,10 +163,7 @@ def rank_projection(x: torch.Tensor, v: torch.Tensor | None, partial: torch.Tens
     T, n = x.shape
     if partial.shape[0] != T or partial.shape[1] % k:
         raise ValueError("partial must be [tokens, splits*k]")
-    splits = partial.shape[1] // k
-    rc = _lib.load().narhip_rank_projection(_p(x), T, n, x.stride(0), _p(v), _p(prepared), k, splits,
-                                            _p(partial), rank_mode, _stream(dev))
-    _lib.check(rc)
+    _ops.rank_projection_out(x, v, prepared, k, rank_mode, partial)
     return partial
 
 
@@ -188,10 +182,7 @@ def rank_projection_f16(x: torch.Tensor, v: torch.Tensor, partial: torch.Tensor)
         raise ValueError(f"v must be [{n}, k], got {tuple(v.shape)}")
     if partial.shape[0] != T or partial.shape[1] % k:
         raise ValueError("partial must be [tokens, splits*k]")
-    splits = partial.shape[1] // k
-    rc = _lib.load().narhip_rank_projection_f16(_p(x), T, n, x.stride(0), _p(v), k, splits, _p(partial),
-                                                _stream(dev))
-    _lib.check(rc)
+    _ops.rank_projection_f16_out(x, v, partial)
     return partial
 
 
@@ -210,7 +201,6 @@ def transform_f16(x: torch.Tensor, w_t: torch.Tensor | None, *, v: torch.Tensor 
     dev = x.device
     T, n = x.shape
     k = 0 if w_t is None else int(w_t.shape[0])
-    splits = 0
     if k:
         _require(w_t, torch.float32, "w_t", dev)
         if w_t.shape[1] != n:
@@ -219,7 +209,6 @@ def transform_f16(x: torch.Tensor, w_t: torch.Tensor | None, *, v: torch.Tensor 
             _require(partial, torch.float32, "partial", dev)
             if partial.shape[0] != T or partial.shape[1] % k:
                 raise ValueError(f"partial must be [{T}, splits*{k}]")
-            splits = partial.shape[1] // k
         else:
             if v is None:
                 raise ValueError("the rank term needs v or partial")
@@ -227,16 +216,11 @@ def transform_f16(x: torch.Tensor, w_t: torch.Tensor | None, *, v: torch.Tensor 
             if tuple(v.shape) != (n, k):
                 raise ValueError(f"v must be [{n}, {k}], got {tuple(v.shape)}")
     if out is None:
-        out = torch.empty((T, n), dtype=torch.float16, device=dev)
-    else:
-        _require(out, torch.float16, "out", dev)
-    lib = _lib.load()
-    ws_bytes = lib.narhip_transform_f16_workspace(T, n, k)
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
-    rc = lib.narhip_transform_f16(_p(x), T, n, x.stride(0), had_q, _p(v) if k else None,
-                                  _p(partial) if k else None, splits, _p(w_t), k, _p(out), _p(ws), ws_bytes,
-                                  _stream(dev))
-    _lib.check(rc)
+        return _ops.transform_f16(x, w_t, v, partial, had_q)
+    _require(out, torch.float16, "out", dev)
+    if tuple(out.shape) != (T, n):
+        raise ValueError(f"out must be [{T}, {n}], got {tuple(out.shape)}")
+    _ops.transform_f16_out(x, w_t, v, partial, had_q, out)
     return out
 
 
@@ -270,15 +254,11 @@ def w4a4_gemm(a_codes: torch.Tensor, a_scales: torch.Tensor, a_zeros: torch.Tens
         if tuple(t.shape) != shape:
             raise ValueError(f"{name} must be {shape}, got {tuple(t.shape)}")
     if out is None:
-        out = torch.empty((T, O), dtype=torch.float32, device=dev)
-    else:
-        _require(out, torch.float32, "out", dev)
-    lib = _lib.load()
-    ws_bytes = lib.narhip_w4a4_workspace(T, O, n)
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
-    rc = lib.narhip_w4a4_gemm(_p(a_codes), _p(a_scales), _p(a_zeros), T, _p(w_codes), _p(w_scales),
-                              _p(w_zeros), O, n, group, _p(out), out.stride(0), _p(ws), ws_bytes, _stream(dev))
-    _lib.check(rc)
+        return _ops.w4a4_gemm(a_codes, a_scales, a_zeros, w_codes, w_scales, w_zeros, group)
+    _require(out, torch.float32, "out", dev)
+    if tuple(out.shape) != (T, O):
+        raise ValueError(f"out must be [{T}, {O}], got {tuple(out.shape)}")
+    _ops.w4a4_gemm_out(a_codes, a_scales, a_zeros, w_codes, w_scales, w_zeros, group, out)
     return out
 
 
@@ -292,19 +272,18 @@ def group_quant(x: torch.Tensor, partial: torch.Tensor | None, w_t: torch.Tensor
     dev = x.device
     T, n = x.shape
     k = 0 if w_t is None else int(w_t.shape[0])
-    splits = 0
     if k:
         _require(w_t, torch.float32, "w_t", dev)
+        if partial is None:
+            raise ValueError("the rank term needs the projection partials")
         _require(partial, torch.float32, "partial", dev)
-        splits = partial.shape[1] // k
+        if partial.shape[0] != T or partial.shape[1] % k:
+            raise ValueError(f"partial must be [{T}, splits*{k}]")
+    for t, name, dt in ((codes, "codes", torch.uint8), (scales, "scales", torch.float16),
+                        (zeros, "zeros", torch.float16)):
+        _require(t, dt, name, dev)
     m, q = hadamard
-    lib = _lib.load()
-    ws_bytes = lib.narhip_rotate_quant_workspace(T, n, m, q, k, n, 1, splits, int(prepared is not None), rank_mode)
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
-    rc = lib.narhip_group_quant(_p(x), T, n, x.stride(0), m, q, _p(partial), splits, k, _p(w_t), _p(prepared),
-                                group, _p(codes), _p(scales), _p(zeros), rank_mode, _p(ws), ws_bytes,
-                                _stream(dev))
-    _lib.check(rc)
+    _ops.group_quant_out(x, partial if k else None, w_t, prepared, m, q, group, rank_mode, codes, scales, zeros)
 
 
 def dequantize(codes: torch.Tensor, scales: torch.Tensor, zeros: torch.Tensor, n: int,
@@ -313,11 +292,7 @@ def dequantize(codes: torch.Tensor, scales: torch.Tensor, zeros: torch.Tensor, n
     _require(codes, torch.uint8, "codes", dev)
     _require(scales, torch.float16, "scales", dev)
     _require(zeros, torch.float16, "zeros", dev)
-    rows = codes.shape[0]
-    out = torch.empty((rows, n), dtype=torch.float32, device=dev)
-    _lib.check(_lib.load().narhip_dequantize(_p(codes), _p(scales), _p(zeros), rows, n, group,
-                                             _p(out), _stream(dev)))
-    return out
+    return _ops.dequantize(codes, scales, zeros, n, group)
 
 
 def mfma_probe(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
