@@ -93,6 +93,28 @@ int narhip_rotate_quant(const void *x_bf16, int64_t tokens, int64_t n, int64_t l
                         float *rotated, const int64_t *dest_rows, int32_t rank_mode,
                         void *workspace, size_t workspace_bytes, void *stream);
 
+/* Allocation-free narhip_rotate_quant.  No counterpart in the reference: it is
+ * for callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  Same arguments and
+ * results as narhip_rotate_quant without the workspace: the scratch the call
+ * needs comes from a per-device array of NARHIP_NOALLOC_SCRATCH_BYTES that the
+ * library holds from its load until the process ends; the MFMA rank path
+ * processes the tokens in chunks (>= 256 tokens) that fit in it.  Arguments
+ * whose scratch still exceeds it (e.g. RANK_EXACT with a Kronecker factor over
+ * more than ~1000 rows of 14336) fail with NARHIP_EWORKSPACE.  The call
+ * allocates nothing and leaves the scratch holding its own data; every byte it
+ * reads there it has written first.  Calls that overlap on one GPU (concurrent
+ * streams, or host threads) share that GPU's scratch and race: serialize them.
+ */
+#define NARHIP_NOALLOC_SCRATCH_BYTES (64ll << 20)
+
+int narhip_rotate_quant_noalloc(const void *x_bf16, int64_t tokens, int64_t n, int64_t ld_x,
+                                int32_t had_m, int32_t had_q, const float *signs,
+                                int32_t k, int64_t rank_block, const float *v, const float *w_t,
+                                const void *prepared, const float *partial, int32_t splits,
+                                int32_t group, uint8_t *codes, void *scales_f16, void *zeros_f16,
+                                float *rotated, const int64_t *dest_rows, int32_t rank_mode, void *stream);
+
 /* Workspace bytes narhip_rotate_quant needs for these arguments (0 when none;
  * have_partial / have_prepared = 1 when the caller passes them). */
 size_t narhip_rotate_quant_workspace(int64_t tokens, int64_t n, int32_t had_m, int32_t had_q,

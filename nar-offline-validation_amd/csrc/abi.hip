@@ -1,6 +1,7 @@
 // extern "C" boundary of libnarhip: argument validation, planning and the
 // entry points of include/narhip.h.  The kernels are launched through the
-// launchers of host.hpp (launch_*.hip); this unit compiles no device code.
+// launchers of host.hpp (launch_*.hip); this unit compiles no kernel.  Its only
+// device object is the scratch array of the allocation-free entry point.
 #include "host.hpp"
 
 #include <cstdarg>
@@ -176,8 +177,10 @@ struct Plan {
     }
 };
 
+// budget > 0: the MFMA rank path halves its token chunk (down to 256 tokens)
+// until the workspace fits in `budget` bytes; the other paths are not chunked.
 int make_plan(int64_t T, int64_t n, int m, int q, int k, int64_t nb, bool have_partial, int splits,
-              bool have_prepared, int rank_mode, Plan &p)
+              bool have_prepared, int rank_mode, Plan &p, size_t budget = 0)
 {
     if (T < 0 || n <= 0) return fail(NARHIP_EINVAL, "tokens %lld / n %lld invalid", (long long)T, (long long)n);
     if (!pow2(q) || q < 128 || q > 1024)
@@ -214,12 +217,21 @@ int make_plan(int64_t T, int64_t n, int m, int q, int k, int64_t nb, bool have_p
         p.need_prep = !have_prepared;
         p.prep_b = p.need_prep ? prepared_bytes(n, k) : 0;
         p.need_proj = !have_partial;
-        p.chunk = chunk_tokens(T, n);
-        p.splits = have_partial ? splits : mfma_splits(p.chunk, n);
-        p.proj_b = p.need_proj ? sizeof(float) * (size_t)p.chunk * (size_t)p.splits * (size_t)k : 0;
         p.need_P = true;
-        p.P_b = sizeof(float) * (size_t)p.chunk * (size_t)n;
-        p.u_b = corr_scratch_bytes(p.chunk, n, k);
+        // the channel splits of the projection follow the unbounded chunk, so a
+        // token's partials, u and output do not depend on the budget
+        p.splits = have_partial ? splits : mfma_splits(chunk_tokens(T, n), n);
+        auto size_chunk = [&](int64_t chunk) {
+            p.chunk = chunk;
+            p.proj_b = p.need_proj ? sizeof(float) * (size_t)chunk * (size_t)p.splits * (size_t)k : 0;
+            p.P_b = sizeof(float) * (size_t)chunk * (size_t)n;
+            p.u_b = corr_scratch_bytes(chunk, n, k);
+        };
+        size_chunk(chunk_tokens(T, n));
+        while (budget && p.total() > budget && p.chunk > 256) {
+            const int64_t half = (p.chunk / 2 + 255) / 256 * 256;
+            size_chunk(half > 256 ? half : 256);
+        }
         return NARHIP_OK;
     }
     p.need_proj = !have_partial;
@@ -250,10 +262,11 @@ int make_plan(int64_t T, int64_t n, int m, int q, int k, int64_t nb, bool have_p
 int run_rotate_quant(const void *x_bf16, int64_t T, int64_t n, int64_t ldx, int m, int q, const float *signs,
                      int k, int64_t nb, const float *v, const float *wt, const void *prepared,
                      const float *partial, int splits, int group, uint8_t *codes, void *scales, void *zeros,
-                     float *rotated, const int64_t *dest, int rank_mode, void *ws, size_t ws_bytes, hipStream_t s)
+                     float *rotated, const int64_t *dest, int rank_mode, void *ws, size_t ws_bytes, hipStream_t s,
+                     size_t budget = 0)
 {
     Plan p;
-    int rc = make_plan(T, n, m, q, k, nb, partial != nullptr, splits, prepared != nullptr, rank_mode, p);
+    int rc = make_plan(T, n, m, q, k, nb, partial != nullptr, splits, prepared != nullptr, rank_mode, p, budget);
     if (rc) return rc;
     if (group != 32 && group != 64 && group != 128) return fail(NARHIP_EUNSUPPORTED, "group %d", group);
     if (q % group) return fail(NARHIP_EINVAL, "group %d must divide the Hadamard block %d", group, q);
@@ -389,6 +402,44 @@ int run_rotate_quant(const void *x_bf16, int64_t T, int64_t n, int64_t ldx, int 
     return launch_seg(a, q, group, p.seg_mode, s);
 }
 
+// ------------------------------------------- allocation-free entry point
+
+// Scratch of narhip_rotate_quant_noalloc: one copy per device, held from the
+// library's load until the process ends.  Host code never passes `scratch`
+// itself to a kernel (on the host it is a stand-in, not a device address):
+// noalloc_scratch looks up each device's address once and every call uses that.
+static __device__ __align__(256) unsigned char scratch[NARHIP_NOALLOC_SCRATCH_BYTES];
+
+constexpr int SCRATCH_MAX_DEVICES = 64;
+
+// The device address of `scratch` on the device that owns stream s (the
+// current device for the null stream), looked up with that device current.
+int noalloc_scratch(hipStream_t s, void **out)
+{
+    static std::mutex mu;
+    static void *addr[SCRATCH_MAX_DEVICES] = {};
+    int cur = 0;
+    hipError_t e = hipGetDevice(&cur);
+    if (e != hipSuccess) return fail(NARHIP_EHIP, "hipGetDevice: %s", hipGetErrorString(e));
+    int dev = cur;
+    if (s && (e = hipStreamGetDevice(s, &dev)) != hipSuccess)
+        return fail(NARHIP_EHIP, "hipStreamGetDevice: %s", hipGetErrorString(e));
+    if (dev < 0 || dev >= SCRATCH_MAX_DEVICES) return fail(NARHIP_EUNSUPPORTED, "device %d", dev);
+    std::lock_guard<std::mutex> lock(mu);
+    if (!addr[dev]) {
+        if (dev != cur && (e = hipSetDevice(dev)) != hipSuccess)
+            return fail(NARHIP_EHIP, "hipSetDevice(%d): %s", dev, hipGetErrorString(e));
+        void *ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (dev != cur) (void)hipSetDevice(cur);
+        if (e != hipSuccess) return fail(NARHIP_EHIP, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+        if (!ptr) return fail(NARHIP_EHIP, "hipGetSymbolAddress(scratch) returned null");
+        addr[dev] = ptr;
+    }
+    *out = addr[dev];
+    return NARHIP_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -447,6 +498,32 @@ int narhip_rotate_quant(const void *x_bf16, int64_t tokens, int64_t n, int64_t l
     return run_rotate_quant(x_bf16, tokens, n, ld_x, had_m, had_q, signs, k, rank_block, v, w_t, prepared,
                             partial, splits, group, codes, scales_f16, zeros_f16, rotated, dest_rows, rank_mode,
                             workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+int narhip_rotate_quant_noalloc(const void *x_bf16, int64_t tokens, int64_t n, int64_t ld_x,
+                                int32_t had_m, int32_t had_q, const float *signs,
+                                int32_t k, int64_t rank_block, const float *v, const float *w_t,
+                                const void *prepared, const float *partial, int32_t splits,
+                                int32_t group, uint8_t *codes, void *scales_f16, void *zeros_f16,
+                                float *rotated, const int64_t *dest_rows, int32_t rank_mode, void *stream)
+{
+    clear_error();
+    const size_t cap = (size_t)NARHIP_NOALLOC_SCRATCH_BYTES;
+    Plan p;
+    if (int rc = make_plan(tokens, n, had_m, had_q, k, rank_block, partial != nullptr, splits,
+                           prepared != nullptr, rank_mode, p, cap))
+        return rc;
+    if (p.total() > cap)
+        return fail(NARHIP_EWORKSPACE,
+                    "these arguments need %zu bytes of scratch; the allocation-free entry point holds %zu "
+                    "(call narhip_rotate_quant with a workspace)", p.total(), cap);
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    void *ws = nullptr;
+    if (p.total() > 0)
+        if (int rc = noalloc_scratch(s, &ws)) return rc;
+    return run_rotate_quant(x_bf16, tokens, n, ld_x, had_m, had_q, signs, k, rank_block, v, w_t, prepared,
+                            partial, splits, group, codes, scales_f16, zeros_f16, rotated, dest_rows, rank_mode,
+                            ws, cap, s, cap);
 }
 
 int narhip_rank_projection(const void *x_bf16, int64_t tokens, int64_t n, int64_t ld_x,

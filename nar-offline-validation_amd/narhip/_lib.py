@@ -23,7 +23,7 @@ RANK_MFMA = 2
 
 EXPORTS = (
     "narhip_abi_version", "narhip_last_error_string", "narhip_paley",
-    "narhip_rotate_quant", "narhip_rotate_quant_workspace",
+    "narhip_rotate_quant", "narhip_rotate_quant_workspace", "narhip_rotate_quant_noalloc",
     "narhip_rank_factors_bytes", "narhip_prepare_rank_factors",
     "narhip_rank_projection", "narhip_group_quant", "narhip_dequantize",
     "narhip_dynamic_asym_int4", "narhip_hadamard_rows", "narhip_transform_f16",
@@ -50,6 +50,7 @@ def load() -> ctypes.CDLL:
         c_p, c_i64, c_i64, c_i64, c_i32, c_i32, c_p,
         c_i32, c_i64, c_p, c_p, c_p, c_p, c_i32,
         c_i32, c_p, c_p, c_p, c_p, c_p, c_i32, c_p, c_sz, c_p]
+    lib.narhip_rotate_quant_noalloc.argtypes = lib.narhip_rotate_quant.argtypes[:-3] + [c_p]
     lib.narhip_rotate_quant_workspace.argtypes = [c_i64, c_i64, c_i32, c_i32, c_i32, c_i64, c_i32, c_i32,
                                                   c_i32, c_i32]
     lib.narhip_rotate_quant_workspace.restype = c_sz
@@ -73,7 +74,8 @@ def load() -> ctypes.CDLL:
     lib.narhip_w4a4_workspace.argtypes = [c_i64, c_i64, c_i64]
     lib.narhip_w4a4_workspace.restype = c_sz
     lib.narhip_mfma_probe.argtypes = [c_p, c_p, c_p, c_p]
-    for name in ("narhip_paley", "narhip_rotate_quant", "narhip_rank_projection", "narhip_prepare_rank_factors",
+    for name in ("narhip_paley", "narhip_rotate_quant", "narhip_rotate_quant_noalloc", "narhip_rank_projection",
+                 "narhip_prepare_rank_factors",
                  "narhip_group_quant", "narhip_dequantize", "narhip_dynamic_asym_int4", "narhip_hadamard_rows",
                  "narhip_transform_f16", "narhip_rank_projection_f16", "narhip_w4a4_gemm", "narhip_mfma_probe"):
         getattr(lib, name).restype = ctypes.c_int

@@ -152,3 +152,19 @@ def test_group_quant_requires_w_t_off_the_mfma_path():
     assert b"w_t" in lib.narhip_last_error_string()
     exact = [16, 4, 14336, 14336, 28, 512, 16, 1, 32, None, 16, 128, 16, 16, 16, 1, None, 0, None]
     assert lib.narhip_group_quant(*exact) == -1
+
+
+def test_noalloc_host_validation():
+    """The allocation-free entry point rejects, before any device work, arguments
+    whose scratch exceeds its array (the exact Kronecker path over 2048 rows of
+    14336 needs a 117 MB correction buffer) and bad shapes like the other one."""
+    import narhip
+    lib = narhip.load()
+    n = 14336
+    assert lib.narhip_rotate_quant_workspace(2048, n, 28, 512, 32, n, 0, 0, 0, 1) > 64 << 20
+    rc = lib.narhip_rotate_quant_noalloc(16, 2048, n, n, 28, 512, None, 32, n, 16, 16, None, None, 0, 128,
+                                         16, 16, 16, None, None, 1, None)
+    assert rc == -4 and b"allocation-free" in lib.narhip_last_error_string()
+    rc = lib.narhip_rotate_quant_noalloc(16, 4, 1000, 1000, 1, 128, None, 0, 1000, None, None, None, None, 0,
+                                         128, 16, 16, 16, None, None, 0, None)
+    assert rc == -1
