@@ -67,7 +67,9 @@ int narhip_paley(int32_t m, int8_t *out_host);
  * launch_nar_fused / launch_hadamard (nar/kernels/r4_fused_v2.py:327-350).
  *
  *   had_m, had_q : Hadamard blocks of had_m*had_q channels get H_m (x) H_q;
- *                  had_m in {1, 12, 28}, had_q a power of two in [128, 1024].
+ *                  had_m in {1, 12, 20, 28}, had_q a power of two in [128, 1024]
+ *                  (H_20: 128 or 256), or had_m = 1, had_q = n in {2048, 4096,
+ *                  8192} (one FWHT over the row, k = 0).
  *                  had_m = 1 with had_q < n is the block Hadamard of nar/kernels;
  *                  had_m > 1 requires had_m*had_q = n (one Kronecker row).
  *   signs        : fp32 [n] or NULL, applied to the Hadamard input only.
@@ -166,11 +168,35 @@ int narhip_dequantize(const uint8_t *codes, const void *scales_f16, const void *
 int narhip_dynamic_asym_int4(const void *x, int32_t dtype, int64_t rows, int64_t n, int32_t group,
                              uint8_t *codes, void *scales_f16, void *zeros_f16, void *deq, void *stream);
 
+/* Rotate, then the hooks' quantizer, in one call: dynamic_asym_int4's tuple
+ * (codes uint8 [tokens, n] one per byte, scales and zeros fp16
+ * [tokens, n/group], deq fp32 [tokens, n]) of x' = H_s x - (x V) W''^T, with the
+ * transform arguments of narhip_rotate_quant (no prepared factors, partials,
+ * destination rows or rotated copy) and any group a power of two in [8, 512]
+ * dividing n.  Replaces the hook sequence full_hadamard_rows or
+ * RotationFactor.apply followed by dynamic_asym_int4
+ * (nar/activation_experiments.py:295-299,603-606; nar/experiment.py:904-906;
+ * nar/e14_w4a4kv4.py:725).  One kernel, reading x once, for groups of 32, 64
+ * or 128 dividing had_q on: block / per-head Hadamards with no rank term or a
+ * per-block rank (rank_block = had_q, k <= 8), the full-row FWHT of
+ * n in {2048, 4096, 8192}, and H_m (x) H_q without a rank term (rank_mode
+ * AUTO or MFMA); otherwise x' is staged in the workspace and quantized by a
+ * second kernel. */
+size_t narhip_rotate_dynamic_asym_int4_workspace(int64_t tokens, int64_t n, int32_t had_m, int32_t had_q,
+                                                 int32_t k, int64_t rank_block, int32_t group, int32_t rank_mode);
+int narhip_rotate_dynamic_asym_int4(const void *x_bf16, int64_t tokens, int64_t n, int64_t ld_x, int32_t had_m,
+                                    int32_t had_q, const float *signs, int32_t k, int64_t rank_block,
+                                    const float *v, const float *w_t, int32_t group, uint8_t *codes,
+                                    void *scales_f16, void *zeros_f16, float *deq, int32_t rank_mode,
+                                    void *workspace, size_t workspace_bytes, void *stream);
+
 /* The Kronecker Hadamard of each row alone, fp32 out [rows, n]:
- * (H_m (x) H_q) diag(signs) x with m in {1, 12, 28} (m = 1: every aligned block
- * of q channels), q in {128, ..., 1024}; signs fp32 [n] or NULL.  Replaces
- * full_hadamard_rows (nar/activation_experiments.py:188-217) for the widths
- * 12 * 2^j and 28 * 2^j and block Hadamards. */
+ * (H_m (x) H_q) diag(signs) x with m in {1, 12, 20, 28} (m = 1: every aligned
+ * block of q channels), q in {128, ..., 1024} (H_20: q in {128, 256}), or
+ * m = 1 with q = n in {2048, 4096, 8192} (one FWHT over the row); signs fp32
+ * [n] or NULL.  Replaces full_hadamard_rows (nar/activation_experiments.py:
+ * 188-217) for the widths 12 * 2^j, 20 * 2^j, 28 * 2^j and 2^j <= 8192, and
+ * block Hadamards. */
 int narhip_hadamard_rows(const void *x_bf16, int64_t rows, int64_t n, int64_t ld_x, int32_t had_m, int32_t had_q,
                          const float *signs, float *out, void *stream);
 

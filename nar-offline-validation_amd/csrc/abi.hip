@@ -64,7 +64,7 @@ int64_t resident_blocks(const void *kernel, int threads, size_t lds)
 // ----------------------------------------------------------- Paley factors
 // Paley I construction: order m = p + 1 from the quadratic residues of a
 // field of p elements; first row and column +1, lower-right block Q - I with
-// Q[r][c] = chi(r - c).  p = 11 uses Z_11; p = 27 uses GF(3^3) with modulus
+// Q[r][c] = chi(r - c).  p = 11 and 19 use Z_p; p = 27 uses GF(3^3) with modulus
 // x^3 + 2x + 1 and elements c0 + 3 c1 + 9 c2 (the encoding the reference's
 // construction uses, so the +-1 pattern is the same matrix).
 
@@ -96,15 +96,18 @@ int gf27_sub(int a, int b)
 int build_paley(int m, int8_t *out)
 {
     if (m == 1) { out[0] = 1; return 0; }
-    if (m != 12 && m != 28) return -1;
+    // Paley I: order p + 1 over Z_p for the primes p = 11, 19 (p = 3 mod 4),
+    // over GF(27) for 28; core entry chi(row - col), bordered by ones, minus I
+    if (m != 12 && m != 20 && m != 28) return -1;
     const int p = m - 1;
+    const bool field = m == 28;
     bool residue[27] = {};
-    for (int v = 1; v < p; v++) residue[m == 12 ? (v * v) % p : gf27_mul(v, v)] = true;
+    for (int v = 1; v < p; v++) residue[field ? gf27_mul(v, v) : (v * v) % p] = true;
     for (int r = 0; r < m; r++)
         for (int c = 0; c < m; c++) {
             int val = 1;
             if (r > 0 && c > 0) {
-                int d = m == 12 ? ((r - c) % p + p) % p : gf27_sub(r - 1, c - 1);
+                int d = field ? gf27_sub(r - 1, c - 1) : ((r - c) % p + p) % p;
                 val = (d == 0 ? 0 : (residue[d] ? 1 : -1)) - (r == c ? 1 : 0);
             }
             out[r * m + c] = (int8_t)val;
@@ -139,7 +142,7 @@ namespace {
 
 // --------------------------------------------------------------- planning
 
-enum Path { PATH_SEG, PATH_SEG_PARTIAL_EXACT, PATH_KRON_EXACT, PATH_KRON_MFMA_QUANT, PATH_MFMA_RANK };
+enum Path { PATH_SEG, PATH_SEG_PARTIAL_EXACT, PATH_KRON_EXACT, PATH_KRON_MFMA_QUANT, PATH_MFMA_RANK, PATH_FWHT };
 
 // The MFMA rank path stages the rotated rows P through memory between the
 // transform and the correction kernels; tokens are processed in chunks so that
@@ -183,9 +186,19 @@ int make_plan(int64_t T, int64_t n, int m, int q, int k, int64_t nb, bool have_p
               bool have_prepared, int rank_mode, Plan &p, size_t budget = 0)
 {
     if (T < 0 || n <= 0) return fail(NARHIP_EINVAL, "tokens %lld / n %lld invalid", (long long)T, (long long)n);
+    if (m == 1 && q == n && fwht_rows_width(q)) {
+        // one FWHT over the whole power-of-two row, no rank term
+        if (k != 0) return fail(NARHIP_EUNSUPPORTED, "rank term over a %d-wide FWHT row not built", q);
+        if (rank_mode < 0 || rank_mode > 2) return fail(NARHIP_EINVAL, "rank_mode %d", rank_mode);
+        p = Plan{};
+        p.path = PATH_FWHT;
+        return NARHIP_OK;
+    }
     if (!pow2(q) || q < 128 || q > 1024)
-        return fail(NARHIP_EUNSUPPORTED, "Hadamard block width %d: need a power of two in [128, 1024]", q);
-    if (m != 1 && m != 12 && m != 28) return fail(NARHIP_EUNSUPPORTED, "no Paley factor of order %d", m);
+        return fail(NARHIP_EUNSUPPORTED,
+                    "Hadamard block width %d: need a power of two in [128, 1024] (or q = n in [2048, 8192])", q);
+    if (m != 1 && m != 12 && m != 20 && m != 28)
+        return fail(NARHIP_EUNSUPPORTED, "no Paley factor of order %d", m);
     if (n % ((int64_t)m * q)) return fail(NARHIP_EINVAL, "n=%lld is not a multiple of %d*%d", (long long)n, m, q);
     if (m > 1 && (int64_t)m * q != n)
         return fail(NARHIP_EUNSUPPORTED, "Kronecker factor must span the row (m*q = n)");
@@ -286,6 +299,14 @@ int run_rotate_quant(const void *x_bf16, int64_t T, int64_t n, int64_t ldx, int 
     if (need > 0 && (!ws || ws_bytes < need))
         return fail(NARHIP_EWORKSPACE, "workspace of %zu bytes required, %zu given", need, ws_bytes);
     if (T == 0) return NARHIP_OK;
+    if (p.path == PATH_FWHT) {
+        FwhtArgs fa{};
+        fa.x = static_cast<const uint16_t *>(x_bf16); fa.ldx = ldx; fa.T = T; fa.signs = signs;
+        fa.rotated = rotated; fa.codes = codes; fa.scales = static_cast<uint16_t *>(scales);
+        fa.zeros = static_cast<uint16_t *>(zeros); fa.dest = dest;
+        fa.sq = f32_sqrt(q); fa.rsq = 1.0f / fa.sq;
+        return launch_fwht(fa, q, group, s);
+    }
 
     char *wsp = static_cast<char *>(ws);
     void *prep = p.need_prep ? wsp : const_cast<void *>(prepared);
@@ -575,6 +596,96 @@ int narhip_dequantize(const uint8_t *codes, const void *scales_f16, const void *
                           rows, n, group, out, static_cast<hipStream_t>(stream));
 }
 
+// The hooks' fused form: one kernel where the transform kernel has the tuple
+// epilogue (block or per-head segments with no rank term or per-block rank,
+// the full-row FWHT, the Kronecker MFMA transform without a rank term);
+// otherwise x' goes through the workspace and the standalone quantizer.
+static bool tuple_one_pass(const Plan &p, int group, int q)
+{
+    if (group != 32 && group != 64 && group != 128) return false;
+    if (q % group) return false;
+    return p.path == PATH_FWHT || p.path == PATH_KRON_MFMA_QUANT || (p.path == PATH_SEG && !p.kron);
+}
+
+static bool tuple_group_ok(int64_t n, int group)
+{
+    return group > 0 && n % group == 0 && group % 8 == 0 && group <= 512 && !(group & (group - 1));
+}
+
+size_t narhip_rotate_dynamic_asym_int4_workspace(int64_t tokens, int64_t n, int32_t had_m, int32_t had_q, int32_t k,
+                                                 int64_t rank_block, int32_t group, int32_t rank_mode)
+{
+    Plan p;
+    if (tokens < 0 || !tuple_group_ok(n, group) ||
+        make_plan(tokens, n, had_m, had_q, k, rank_block, false, 0, false, rank_mode, p))
+        return 0;
+    if (tuple_one_pass(p, group, had_q)) return 0;
+    const size_t T = (size_t)tokens, N = (size_t)n;
+    return align256(p.total()) + align256(4 * T * N) + align256(T * N / 2) + 2 * align256(2 * T * (N / 128));
+}
+
+int narhip_rotate_dynamic_asym_int4(const void *x_bf16, int64_t tokens, int64_t n, int64_t ld_x, int32_t had_m,
+                                    int32_t had_q, const float *signs, int32_t k, int64_t rank_block, const float *v,
+                                    const float *w_t, int32_t group, uint8_t *codes, void *scales_f16,
+                                    void *zeros_f16, float *deq, int32_t rank_mode, void *workspace,
+                                    size_t workspace_bytes, void *stream)
+{
+    clear_error();
+    Plan p;
+    if (int rc = make_plan(tokens, n, had_m, had_q, k, rank_block, false, 0, false, rank_mode, p)) return rc;
+    if (!tuple_group_ok(n, group))
+        return fail(NARHIP_EINVAL, "group size %d: need a power of two in [8, 512] dividing %lld", group,
+                    (long long)n);
+    if (ld_x < n || ld_x % 8) return fail(NARHIP_EINVAL, "ld_x=%lld must be >= n and a multiple of 8", (long long)ld_x);
+    if (tokens == 0) return NARHIP_OK;
+    if (!x_bf16 || !codes || !scales_f16 || !zeros_f16 || !deq) return fail(NARHIP_EINVAL, "null tensor argument");
+    if (!aligned16(x_bf16) || !aligned16(deq) || (reinterpret_cast<uintptr_t>(codes) & 7u))
+        return fail(NARHIP_EINVAL, "x and deq must be 16-byte aligned, codes 8-byte aligned");
+    if (k > 0 && (!v || !w_t)) return fail(NARHIP_EINVAL, "rank factors missing");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const uint16_t *x = static_cast<const uint16_t *>(x_bf16);
+    uint16_t *sc = static_cast<uint16_t *>(scales_f16), *zc = static_cast<uint16_t *>(zeros_f16);
+    if (tuple_one_pass(p, group, had_q)) {
+        if (p.path == PATH_FWHT) {
+            FwhtArgs fa{};
+            fa.x = x; fa.ldx = ld_x; fa.T = tokens; fa.signs = signs;
+            fa.codes = codes; fa.scales = sc; fa.zeros = zc; fa.deq = deq;
+            fa.sq = f32_sqrt(had_q); fa.rsq = 1.0f / fa.sq;
+            return launch_fwht(fa, had_q, group, s);
+        }
+        if (p.path == PATH_KRON_MFMA_QUANT) {
+            KronArgs ka{};
+            ka.x = x; ka.ldx = ld_x; ka.T = tokens; ka.n = n; ka.signs = signs;
+            ka.codes = codes; ka.scales = sc; ka.zeros = zc; ka.deq = deq;
+            ka.paley = paley_table(had_m); ka.sq = f32_sqrt(had_q); ka.rsq = 1.0f / ka.sq;
+            ka.hm = 1.0f / f32_sqrt(had_m);
+            return launch_kron(nullptr, &ka, true, had_m, had_q, group, s);
+        }
+        SegArgs sa{};
+        sa.x = x; sa.ldx = ld_x; sa.T = tokens; sa.n = n; sa.signs = signs; sa.v = v; sa.wt = w_t; sa.k = k;
+        sa.codes = codes; sa.scales = sc; sa.zeros = zc; sa.deq = deq;
+        sa.sq = f32_sqrt(had_q); sa.rsq = 1.0f / sa.sq;
+        return launch_seg(sa, had_q, group, p.seg_mode, s);
+    }
+    // two passes: the fused operator into the workspace (x' in fp32; its own
+    // group-128 codes are scratch), then the hooks' quantizer on x'
+    const size_t T = (size_t)tokens, N = (size_t)n;
+    const size_t need = narhip_rotate_dynamic_asym_int4_workspace(tokens, n, had_m, had_q, k, rank_block, group,
+                                                                  rank_mode);
+    if (!workspace || workspace_bytes < need)
+        return fail(NARHIP_EWORKSPACE, "workspace of %zu bytes required, %zu given", need, workspace_bytes);
+    char *w = static_cast<char *>(workspace);
+    const size_t rq = p.total();
+    float *rot = reinterpret_cast<float *>(w + align256(rq));
+    uint8_t *pc = reinterpret_cast<uint8_t *>(rot) + align256(4 * T * N);
+    uint16_t *ps = reinterpret_cast<uint16_t *>(pc + align256(T * N / 2));
+    uint16_t *pz = reinterpret_cast<uint16_t *>(reinterpret_cast<char *>(ps) + align256(2 * T * (N / 128)));
+    if (int rc = run_rotate_quant(x_bf16, tokens, n, ld_x, had_m, had_q, signs, k, rank_block, v, w_t, nullptr,
+                                  nullptr, 0, 128, pc, ps, pz, rot, nullptr, rank_mode, rq ? w : nullptr, rq, s))
+        return rc;
+    return launch_quant_tuple(DT_F32, rot, tokens * n, group, codes, sc, zc, deq, s);
+}
+
 int narhip_dynamic_asym_int4(const void *x, int32_t dtype, int64_t rows, int64_t n, int32_t group,
                              uint8_t *codes, void *scales_f16, void *zeros_f16, void *deq, void *stream)
 {
@@ -598,9 +709,12 @@ int narhip_hadamard_rows(const void *x_bf16, int64_t rows, int64_t n, int64_t ld
 {
     clear_error();
     if (rows < 0 || n <= 0) return fail(NARHIP_EINVAL, "bad shape rows=%lld n=%lld", (long long)rows, (long long)n);
-    if (!pow2(had_q) || had_q < 128 || had_q > 1024)
-        return fail(NARHIP_EUNSUPPORTED, "Hadamard block width %d: need a power of two in [128, 1024]", had_q);
-    if (had_m != 1 && had_m != 12 && had_m != 28) return fail(NARHIP_EUNSUPPORTED, "no Paley factor of order %d", had_m);
+    const bool full = had_m == 1 && had_q == n && fwht_rows_width(n);
+    if (!full && (!pow2(had_q) || had_q < 128 || had_q > 1024))
+        return fail(NARHIP_EUNSUPPORTED,
+                    "Hadamard block width %d: need a power of two in [128, 1024] (or q = n in [2048, 8192])", had_q);
+    if (had_m != 1 && had_m != 12 && had_m != 20 && had_m != 28)
+        return fail(NARHIP_EUNSUPPORTED, "no Paley factor of order %d", had_m);
     if ((int64_t)had_m * had_q != n && !(had_m == 1 && n % had_q == 0))
         return fail(NARHIP_EUNSUPPORTED, "H_%d x H_%d does not tile a row of %lld", had_m, had_q, (long long)n);
     if (ld_x < n || ld_x % 8) return fail(NARHIP_EINVAL, "ld_x=%lld must be >= n and a multiple of 8", (long long)ld_x);
@@ -609,6 +723,12 @@ int narhip_hadamard_rows(const void *x_bf16, int64_t rows, int64_t n, int64_t ld
     if (!aligned16(x_bf16) || !aligned16(out)) return fail(NARHIP_EINVAL, "x and out must be 16-byte aligned");
     hipStream_t s = static_cast<hipStream_t>(stream);
     const uint16_t *x = static_cast<const uint16_t *>(x_bf16);
+    if (full) {
+        FwhtArgs fa{};
+        fa.x = x; fa.ldx = ld_x; fa.T = rows; fa.signs = signs; fa.rotated = out;
+        fa.sq = f32_sqrt(had_q); fa.rsq = 1.0f / fa.sq;
+        return launch_fwht(fa, had_q, 128, s);
+    }
     if (had_m > 1) {
         KronArgs ka{};
         ka.x = x; ka.ldx = ld_x; ka.T = rows; ka.n = n; ka.signs = signs; ka.P = out;

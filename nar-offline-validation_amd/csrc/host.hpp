@@ -9,6 +9,7 @@
 #include "../../include/narhip.h"
 #include "corr_quant.hip"
 #include "dequant.hip"
+#include "fwht_rows.hip"
 #include "hooks.hip"
 #include "kron_mfma.hip"
 #include "mfma.hpp"
@@ -133,6 +134,9 @@ inline size_t xf_pd_bytes(int64_t T, int S) { return align256(sizeof(double) * X
 
 // launch_seg.hip
 int launch_seg(const SegArgs &a, int q, int b, int mode, hipStream_t s);
+// full-row FWHT of n = q in {2048, 4096, 8192} channels (fwht_rows.hip)
+inline bool fwht_rows_width(int64_t q) { return q == 2048 || q == 4096 || q == 8192; }
+int launch_fwht(const FwhtArgs &a, int q, int b, hipStream_t s);
 int launch_seg_f16(const SegArgs &a, int q, int k, hipStream_t s);
 
 // launch_kron.hip: exact rq_row (RowArgs) when ra, else kron_mfma (KronArgs)

@@ -27,6 +27,7 @@ struct KronArgs {
     float *rotated;
     PaleyTable paley;
     float sq, rsq, hm;     // fp32(sqrt(Q)), RN(1/sq), RN(1/fp32(sqrt(M)))
+    float *deq;            // fp32 [rows, n]: the hooks' tuple (codes unpacked [rows, n]), or null
 };
 
 // F in LDS: row a of the token's M x Q block at a * Q, column c stored at
@@ -119,6 +120,12 @@ kron_mfma_kernel(KronArgs a)
         }
         if (a.signs) apply_signs<NH>(v, a.signs + s * Q + chunk * 8);
         fwht_lane_stages<NH>(v);
+        if constexpr (NH == 1) {
+            // Q = 128: one 8-value block per cross-lane stage, too few for the
+            // fused DPP form below; plain butterflies and the checked division
+            fwht_xlane_plain(v, sj);
+            div_sqrt_q<Q>(v, a.sq, a.rsq);
+        } else {
         // cross-lane stages as one v_fmac with a DPP source: v + s_j * partner.
         // The lower lane of each pair holds the sum, the upper lane the negated
         // difference, so after the four stages the lane holds sigma * (true
@@ -148,6 +155,7 @@ kron_mfma_kernel(KronArgs a)
             for (int i = 0; i < NV; i++) v[i] = v[i] / a.sq;
         } else {
             div_sqrt_q_fast<Q>(v, sigma * a.sq, sigma * a.rsq);
+        }
         }
 #pragma unroll
         for (int h = 0; h < NH; h++) {
@@ -272,10 +280,13 @@ kron_mfma_kernel(KronArgs a)
                 v[0] = p0.x; v[1] = p0.y; v[2] = p0.z; v[3] = p0.w;
                 v[4] = p1.x; v[5] = p1.y; v[6] = p1.z; v[7] = p1.w;
             }
-            GroupParams gp;
-        const uint32_t word = quant_group8<G8>(v, gp);
+                GroupParams gp;
+            const uint32_t word = quant_group8<G8>(v, gp);
             if (ok) {
-                *reinterpret_cast<uint32_t *>(a.codes + orow * (N / 2) + ch * 4) = word;
+                if (a.deq)
+                    store_tuple8(v, gp, word, a.codes + orow * N + ch * 8, a.deq + orow * N + ch * 8);
+                else
+                    *reinterpret_cast<uint32_t *>(a.codes + orow * (N / 2) + ch * 4) = word;
                 if ((ch % G8) == 0) {
                     const int64_t gi = orow * (N / B) + (ch * 8) / B;
                     a.scales[gi] = gp.s16;

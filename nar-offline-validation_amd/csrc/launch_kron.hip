@@ -59,12 +59,22 @@ int launch_kron_m(const RowArgs *ra, const KronArgs *ka, bool quant, int q, int 
     return fail(NARHIP_EUNSUPPORTED, "Kronecker H_%d x H_%d not built", M, q);
 }
 
+// H_20 (x) H_q: the Qwen3 widths 2560 = 20 x 128 and 5120 = 20 x 256
+int launch_kron_20(const RowArgs *ra, const KronArgs *ka, bool quant, int q, int b, hipStream_t s)
+{
+    switch (q) {
+    case 128: return launch_kron_mq<20, 128>(ra, ka, quant, b, s);
+    case 256: return launch_kron_mq<20, 256>(ra, ka, quant, b, s);
+    }
+    return fail(NARHIP_EUNSUPPORTED, "Kronecker H_20 x H_%d not built", q);
+}
 
 }  // namespace
 
 int launch_kron(const RowArgs *ra, const KronArgs *ka, bool quant, int m, int q, int b, hipStream_t s)
 {
     if (m == 12) return launch_kron_m<12>(ra, ka, quant, q, b, s);
+    if (m == 20) return launch_kron_20(ra, ka, quant, q, b, s);
     if (m == 28) return launch_kron_m<28>(ra, ka, quant, q, b, s);
     return fail(NARHIP_EUNSUPPORTED, "Paley order %d not built", m);
 }

@@ -49,6 +49,35 @@ int launch_seg(const SegArgs &a, int q, int b, int mode, hipStream_t s)
     return fail(NARHIP_EUNSUPPORTED, "segment width %d not built", q);
 }
 
+namespace {
+
+template <int L>
+int launch_fwht_l(const FwhtArgs &a, int b, hipStream_t s)
+{
+    const dim3 grid((unsigned)a.T);
+    switch (b) {
+    case 32: hipLaunchKernelGGL((fwht_rows_kernel<L, 32>), grid, dim3(256), 0, s, a); break;
+    case 64: hipLaunchKernelGGL((fwht_rows_kernel<L, 64>), grid, dim3(256), 0, s, a); break;
+    case 128: hipLaunchKernelGGL((fwht_rows_kernel<L, 128>), grid, dim3(256), 0, s, a); break;
+    default: return fail(NARHIP_EUNSUPPORTED, "group %d not built", b);
+    }
+    return check_launch("fwht_rows_kernel");
+}
+
+}  // namespace
+
+int launch_fwht(const FwhtArgs &a, int q, int b, hipStream_t s)
+{
+    if (a.T == 0) return NARHIP_OK;
+    if (a.T > 0x7fffffff) return fail(NARHIP_EUNSUPPORTED, "too many rows");
+    switch (q) {
+    case 2048: return launch_fwht_l<11>(a, b, s);
+    case 4096: return launch_fwht_l<12>(a, b, s);
+    case 8192: return launch_fwht_l<13>(a, b, s);
+    }
+    return fail(NARHIP_EUNSUPPORTED, "FWHT row width %d not built", q);
+}
+
 // fp16 rows in and out (E28's transform for block widths other than the fast
 // q = 128 path): the rank term from fp32 partials or folded u (a.partial).
 int launch_seg_f16(const SegArgs &a, int q, int k, hipStream_t s)

@@ -425,6 +425,32 @@ __device__ __forceinline__ uint32_t quant_group8(const float *v, GroupParams &g)
     return word;
 }
 
+// The hooks' tuple for one lane's 8 consecutive elements of a group
+// (dynamic_asym_int4, nar/experiment.py:158-184): the codes of `word` unpacked
+// one per byte, and deq = RN(RN(q s) + z) in fp32 -- NaN where the reference's
+// quotient (x - z) / s is NaN (NaN x or zero-point, Inf - Inf, Inf / Inf with an
+// infinite scale), whose code is 0.  codes 8-byte and deq 16-byte aligned.
+__device__ __forceinline__ void store_tuple8(const float *v, const GroupParams &g, uint32_t word, uint8_t *codes,
+                                             float *deq)
+{
+    float d[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        const float r = v[e] - g.z;
+        const bool nanq = r != r || (__builtin_isinf(r) && __builtin_isinf(g.s));
+        const float q = (float)((word >> (4 * e)) & 15u);
+        d[e] = nanq ? __builtin_nanf("") : __fadd_rn(__fmul_rn(q, g.s), g.z);
+    }
+    // nibble pairs -> one byte each: 0x0000000H -> byte lanes
+    const uint32_t lo = (word & 0xfu) | ((word & 0xf0u) << 4) | ((word & 0xf00u) << 8) | ((word & 0xf000u) << 12);
+    const uint32_t w2 = word >> 16;
+    const uint32_t hi = (w2 & 0xfu) | ((w2 & 0xf0u) << 4) | ((w2 & 0xf00u) << 8) | ((w2 & 0xf000u) << 12);
+    *reinterpret_cast<uint2 *>(codes) = make_uint2(lo, hi);
+    float4 *o = reinterpret_cast<float4 *>(deq);
+    o[0] = make_float4(d[0], d[1], d[2], d[3]);
+    o[1] = make_float4(d[4], d[5], d[6], d[7]);
+}
+
 // ------------------------------------------------- division by fp32(sqrt Q) --
 //
 // v[i] <- RN(v[i] / c) with c = fp32(sqrt(Q)), rc = RN(1/c).

@@ -27,12 +27,13 @@ struct SegArgs {
     const float *partial;   // [T, splits*k] (RANK_PARTIAL)
     int splits;
     int k;
-    uint8_t *codes;         // [rows_out, n/2]
+    uint8_t *codes;         // [rows_out, n/2], or unpacked [rows_out, n] when deq is set
     uint16_t *scales;       // [rows_out, n/B]
     uint16_t *zeros;
     const int64_t *dest;    // [T] output row per token, or null
     float *rotated;         // [T, n] or null
     float sq, rsq;          // fp32(sqrt(Q)) and RN(1/sq), computed on the host
+    float *deq;             // fp32 [rows_out, n]: the hooks' tuple output (unpacked codes), or null
 };
 
 // F16IO: fp16 rows in, fp16 rows out (the E28 transform epilogue: no
@@ -168,7 +169,8 @@ rq_seg_kernel(SegArgs a)
         }
     }
 
-    // ---- quantize groups of B and store (codes == null: rotation only, into `rotated`)
+    // ---- quantize groups of B and store (codes == null: rotation only, into
+    // `rotated`; deq set: the hooks' tuple, codes unpacked)
     if (!a.codes) return;
     const int64_t orow = a.dest ? a.dest[t] : t;
     const int64_t gpt = a.n / B;   // groups per token
@@ -178,7 +180,10 @@ rq_seg_kernel(SegArgs a)
         const uint32_t word = quant_group8<G8>(v + h * 8, g);
         if (active) {
             const int64_t pos = base + h * 128 + chunk * 8;
-            *reinterpret_cast<uint32_t *>(a.codes + orow * (a.n / 2) + pos / 2) = word;
+            if (a.deq)
+                store_tuple8(v + h * 8, g, word, a.codes + orow * a.n + pos, a.deq + orow * a.n + pos);
+            else
+                *reinterpret_cast<uint32_t *>(a.codes + orow * (a.n / 2) + pos / 2) = word;
             if ((chunk & (G8 - 1)) == 0) {
                 const int64_t gi = orow * gpt + pos / B;
                 a.scales[gi] = g.s16;

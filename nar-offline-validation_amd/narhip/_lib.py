@@ -26,7 +26,8 @@ EXPORTS = (
     "narhip_rotate_quant", "narhip_rotate_quant_workspace", "narhip_rotate_quant_noalloc",
     "narhip_rank_factors_bytes", "narhip_prepare_rank_factors",
     "narhip_rank_projection", "narhip_group_quant", "narhip_dequantize",
-    "narhip_dynamic_asym_int4", "narhip_hadamard_rows", "narhip_transform_f16",
+    "narhip_dynamic_asym_int4", "narhip_rotate_dynamic_asym_int4", "narhip_rotate_dynamic_asym_int4_workspace",
+    "narhip_hadamard_rows", "narhip_transform_f16",
     "narhip_transform_f16_workspace", "narhip_rank_projection_f16", "narhip_w4a4_gemm", "narhip_w4a4_workspace",
     "narhip_mfma_probe",
 )
@@ -63,6 +64,11 @@ def load() -> ctypes.CDLL:
         c_p, c_p, c_p, c_i32, c_p, c_sz, c_p]
     lib.narhip_dequantize.argtypes = [c_p, c_p, c_p, c_i64, c_i64, c_i32, c_p, c_p]
     lib.narhip_dynamic_asym_int4.argtypes = [c_p, c_i32, c_i64, c_i64, c_i32, c_p, c_p, c_p, c_p, c_p]
+    lib.narhip_rotate_dynamic_asym_int4.argtypes = [c_p, c_i64, c_i64, c_i64, c_i32, c_i32, c_p, c_i32, c_i64,
+                                                    c_p, c_p, c_i32, c_p, c_p, c_p, c_p, c_i32, c_p, c_sz, c_p]
+    lib.narhip_rotate_dynamic_asym_int4_workspace.argtypes = [c_i64, c_i64, c_i32, c_i32, c_i32, c_i64, c_i32,
+                                                              c_i32]
+    lib.narhip_rotate_dynamic_asym_int4_workspace.restype = c_sz
     lib.narhip_hadamard_rows.argtypes = [c_p, c_i64, c_i64, c_i64, c_i32, c_i32, c_p, c_p, c_p]
     lib.narhip_transform_f16.argtypes = [c_p, c_i64, c_i64, c_i64, c_i32, c_p, c_p, c_i32, c_p, c_i32, c_p, c_p,
                                          c_sz, c_p]
@@ -76,7 +82,8 @@ def load() -> ctypes.CDLL:
     lib.narhip_mfma_probe.argtypes = [c_p, c_p, c_p, c_p]
     for name in ("narhip_paley", "narhip_rotate_quant", "narhip_rotate_quant_noalloc", "narhip_rank_projection",
                  "narhip_prepare_rank_factors",
-                 "narhip_group_quant", "narhip_dequantize", "narhip_dynamic_asym_int4", "narhip_hadamard_rows",
+                 "narhip_group_quant", "narhip_dequantize", "narhip_dynamic_asym_int4",
+                 "narhip_rotate_dynamic_asym_int4", "narhip_hadamard_rows",
                  "narhip_transform_f16", "narhip_rank_projection_f16", "narhip_w4a4_gemm", "narhip_mfma_probe"):
         getattr(lib, name).restype = ctypes.c_int
     _lib = lib

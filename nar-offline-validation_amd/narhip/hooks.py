@@ -11,12 +11,16 @@ HIP kernels of libnarhip.so:
       nar/experiment.py:158-184.  deq in x.dtype and x's shape; scale16 and
       zero16 fp16 [..., G]; codes uint8 [..., G, group_size] (one per byte).
   full_hadamard_rows(x, signs) -> (H_m (x) H_q) diag(signs) x, x's shape
-      nar/activation_experiments.py:188-217, for widths 28 * 2^j, 12 * 2^j and
-      2^j <= 1024.  The kernels read bf16 rows: x must be bf16, or fp32 holding
-      bf16 values (the hooks pass ``value.float()`` of a bf16 model).
-  rotate_dynamic_asym_int4(x, group_size, *, signs=None, v=None, w_t=None)
-      both in one call, with the optional full-row rank-k term x' = Hx + U(V^T x)
-      (w_t = W''^T = -U^T), returning dynamic_asym_int4's tuple of x'.
+      nar/activation_experiments.py:188-217, for widths 28 * 2^j, 12 * 2^j,
+      20 * 2^j (j = 7, 8) and 2^j <= 8192 (the Qwen3 orders 68, 76 and 200
+      are not built and raise).  The kernels read bf16 rows: x must be bf16,
+      or fp32 holding bf16 values (the hooks pass ``value.float()`` of a bf16
+      model).
+  rotate_dynamic_asym_int4(x, group_size, *, signs=None, v=None, w_t=None,
+                           block=None, rank_block=None)
+      both in one call -- full-row or per-block (per-head) Hadamard, optional
+      rank-k term x' = Hx + U(V^T x) over the row or per block (w_t = W''^T =
+      -U^T) -- returning dynamic_asym_int4's tuple of x'.
 
 Device tensors only; there is no CPU path.
 """
@@ -25,7 +29,7 @@ from __future__ import annotations
 
 import torch
 
-from .ops import _ops, hadamard_factors, rotate_quant
+from .ops import RANK_AUTO, _ops, _require, hadamard_factors
 
 _DTYPES = (torch.float32, torch.bfloat16, torch.float16)
 
@@ -78,15 +82,42 @@ def full_hadamard_rows(x: torch.Tensor, signs: torch.Tensor | None) -> torch.Ten
 
 
 def rotate_dynamic_asym_int4(x: torch.Tensor, group_size: int, *, signs: torch.Tensor | None = None,
-                             v: torch.Tensor | None = None, w_t: torch.Tensor | None = None):
-    """dynamic_asym_int4 of x' = (H_m (x) H_q) diag(signs) x + U (V^T x); tuple of x' in fp32."""
+                             v: torch.Tensor | None = None, w_t: torch.Tensor | None = None,
+                             block: int | None = None, rank_block: int | None = None,
+                             rank_mode: int = RANK_AUTO):
+    """dynamic_asym_int4 of x' = H diag(signs) x + U (V^T x); the tuple of x' in fp32.
+
+    H is full_hadamard_rows' construction over the last dimension (block None)
+    or the block-diagonal H_block (e.g. block = head_dim: one H per head).  The
+    rank term takes v fp32 [n, k] and w_t = W''^T = -U^T fp32 [k, n], over the
+    whole row (rank_block None) or per block (rank_block = block: per-head
+    factors stacked along n, k <= 8).  One kernel reads x once and writes the
+    tuple for the block and per-head forms, the power-of-two widths and the
+    Kronecker widths without a rank term (groups of 32, 64 or 128).
+    """
     if not x.is_cuda:
         raise ValueError("rotate_dynamic_asym_int4 (narhip) takes device tensors")
     n = x.shape[-1]
     _group_view_check(n, group_size)
-    m, q = hadamard_factors(n)
+    if block is None:
+        m, q = hadamard_factors(n)
+    else:
+        if n % block:
+            raise ValueError(f"last dimension {n} is not a multiple of the Hadamard block {block}")
+        m, q = 1, int(block)
     xb = _as_bf16_rows(x)
-    rot = torch.empty(xb.shape, dtype=torch.float32, device=x.device)
-    rotate_quant(xb, hadamard=(m, q), signs=_signs_f32(signs, n, x.device), v=v, w_t=w_t,
-                 group=128, rotated=rot)
-    return dynamic_asym_int4(rot.view(x.shape), group_size)
+    k = 0 if w_t is None else int(w_t.shape[0])
+    if k:
+        if v is None:
+            raise ValueError("the rank term needs v and w_t")
+        _require(v, torch.float32, "v", x.device)
+        _require(w_t, torch.float32, "w_t", x.device)
+        if tuple(v.shape) != (n, k) or tuple(w_t.shape) != (k, n):
+            raise ValueError(f"v must be [{n}, {k}] and w_t [{k}, {n}]")
+    nb = n if rank_block is None else int(rank_block)
+    deq, scale, zero, codes = _ops.rotate_dynamic_asym_int4(xb, m, q, _signs_f32(signs, n, x.device), v, w_t, nb,
+                                                            group_size, rank_mode)
+    lead = tuple(x.shape[:-1])
+    groups = n // group_size
+    return (deq.view(x.shape), scale.view(lead + (groups,)), zero.view(lead + (groups,)),
+            codes.view(lead + (groups, group_size)))

@@ -279,6 +279,37 @@ def _(x, group_size):
     return _int4_tuple_like(x, group_size)
 
 
+def _rotated_tuple_like(x: Tensor, group: int):
+    T, n = x.shape
+    return (x.new_empty((T, n), dtype=torch.float32),
+            x.new_empty((T, n // group), dtype=torch.float16),
+            x.new_empty((T, n // group), dtype=torch.float16),
+            x.new_empty((T, n), dtype=torch.uint8))
+
+
+@torch.library.custom_op("narhip::rotate_dynamic_asym_int4", mutates_args=(), device_types=DEVICE)
+def rotate_dynamic_asym_int4(x: Tensor, m: int, q: int, signs: Optional[Tensor], v: Optional[Tensor],
+                             w_t: Optional[Tensor], rank_block: int, group: int,
+                             rank_mode: int) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """dynamic_asym_int4's tuple (deq fp32 [T, n], scale fp16 [T, n/group], zero, codes uint8 [T, n])
+    of x' = (H_m (x) H_q) diag(signs) x - (x V) W''^T for bf16 rows x [T, n]."""
+    T, n = x.shape
+    k = _rank(w_t)
+    deq, scales, zeros, codes = _rotated_tuple_like(x, group)
+    lib = _lib.load()
+    ws_bytes = lib.narhip_rotate_dynamic_asym_int4_workspace(T, n, m, q, k, rank_block, group, rank_mode)
+    ws = _workspace(ws_bytes, x)
+    _lib.check(lib.narhip_rotate_dynamic_asym_int4(_p(x), T, n, x.stride(0), m, q, _p(signs), k, rank_block, _p(v),
+                                                   _p(w_t), group, _p(codes), _p(scales), _p(zeros), _p(deq),
+                                                   rank_mode, _p(ws), ws_bytes, _stream(x)))
+    return deq, scales, zeros, codes
+
+
+@rotate_dynamic_asym_int4.register_fake
+def _(x, m, q, signs, v, w_t, rank_block, group, rank_mode):
+    return _rotated_tuple_like(x, group)
+
+
 @torch.library.custom_op("narhip::hadamard_rows", mutates_args=(), device_types=DEVICE)
 def hadamard_rows(x: Tensor, m: int, q: int, signs: Optional[Tensor]) -> Tensor:
     """fp32 [R, n] = (H_m (x) H_q) diag(signs) x of bf16 rows [R, n], n = m q."""

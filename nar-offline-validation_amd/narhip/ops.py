@@ -40,15 +40,28 @@ def _require(t: torch.Tensor, dtype: torch.dtype, name: str, device: torch.devic
         raise ValueError(f"{name} must be contiguous")
 
 
+QWEN3_PALEY_ORDERS = (20, 68, 76, 200)
+
+
 def hadamard_factors(n: int) -> tuple[int, int]:
     """(m, q) with n = m*q in the dispatch order of full_hadamard_rows
-    (nar/activation_experiments.py:190-201): 28 * 2^j first, then 12 * 2^j,
-    then a power of two."""
+    (nar/activation_experiments.py:188-217): 28 * 2^j first, then 12 * 2^j,
+    then, for widths that are not a power of two, the Qwen3 Paley orders
+    20, 68, 76 and 200 times 2^j, then a power of two.  The kernels build
+    m in {1, 12, 20, 28}; the other orders are rejected by the library."""
+    def pow2(v: int) -> bool:
+        return v >= 1 and not v & (v - 1)
+
     for m in (28, 12):
         q, r = divmod(n, m)
-        if not r and q >= 1 and not q & (q - 1):
+        if not r and pow2(q):
             return m, q
-    if n > 0 and not n & (n - 1):
+    if not pow2(n):
+        for m in QWEN3_PALEY_ORDERS:
+            q, r = divmod(n, m)
+            if not r and pow2(q):
+                return m, q
+    if pow2(n):
         return 1, n
     raise ValueError(f"no frozen full-Hadamard construction for n={n}")
 

@@ -128,13 +128,62 @@ static int gf27_sub(int a, int b)
     return r;
 }
 
+static int is_prime(int q)
+{
+    if (q < 2) return 0;
+    for (int d = 2; d * d <= q; d++) if (q % d == 0) return 0;
+    return 1;
+}
+
+/* chi(d) over Z_q: 0 for d = 0, +1 for a quadratic residue, -1 otherwise. */
+static int chi_mod(int d, int q)
+{
+    d = ((d % q) + q) % q;
+    if (d == 0) return 0;
+    for (int v = 1; v < q; v++) if ((v * v) % q == d) return 1;
+    return -1;
+}
+
+/* Paley's constructions over Z_q for the Qwen3 orders
+ * (nar/activation_experiments.py:141-185): Paley I for a prime q = order - 1
+ * = 3 (mod 4) (ones bordering Q - I, Q[r][c] = chi(r - c)); Paley II for a
+ * prime q = order/2 - 1 = 1 (mod 4) (C the conference matrix bordering Q with
+ * ones and a zero corner, H = [[C + I, C - I], [C - I, -C - I]]). */
+static int paley_zq(int m, int8_t *out)
+{
+    int q = m - 1;
+    if (is_prime(q) && q % 4 == 3) {
+        for (int r = 0; r < m; r++)
+            for (int c = 0; c < m; c++)
+                out[r * m + c] = (int8_t)((r == 0 || c == 0) ? 1 : chi_mod(r - c, q) - (r == c));
+        return 0;
+    }
+    q = m / 2 - 1;
+    if (m % 2 || !is_prime(q) || q % 4 != 1) return -1;
+    const int h = q + 1;
+    for (int r = 0; r < m; r++)
+        for (int c = 0; c < m; c++) {
+            const int rr = r % h, cc = c % h;
+            const int conf = (rr == 0 && cc == 0) ? 0 : (rr == 0 || cc == 0) ? 1 : chi_mod(rr - cc, q);
+            const int eye = rr == cc;
+            int val;
+            if (r < h && c < h) val = conf + eye;
+            else if (r < h || c < h) val = conf - eye;
+            else val = -conf - eye;
+            out[r * m + c] = (int8_t)val;
+        }
+    return 0;
+}
+
 /* Fill out[m*m] with the +-1 Paley Hadamard matrix of order m (row-major,
  * row = output index).  Supports m = 1 (trivial), 12 (Paley I over Z_11,
- * nar/extended_experiment.py:459-472) and 28 (Paley I over GF(27),
- * nar/activation_experiments.py:114-128).  Returns 0 or -1. */
+ * nar/extended_experiment.py:459-472), 28 (Paley I over GF(27),
+ * nar/activation_experiments.py:114-128) and the Qwen3 orders 20, 68, 76 and
+ * 200 (paley_zq).  Returns 0 or -1. */
 int nar_oracle_paley(int m, int8_t *out)
 {
     if (m == 1) { out[0] = 1; return 0; }
+    if (m == 20 || m == 68 || m == 76 || m == 200) return paley_zq(m, out);
     if (m != 12 && m != 28) return -1;
     int q = m - 1;
     int residue[27];
@@ -188,20 +237,24 @@ int nar_oracle_rotate(const float *x, int64_t T, int64_t n, int64_t ldx,
                       float *out, int64_t ldo)
 {
     if (T < 0 || n <= 0 || ldx < n || ldo < n || !is_pow2(q)) return -1;
-    if (m != 1 && m != 12 && m != 28) return -1;
     int64_t blk = (int64_t)m * q;
-    if (n % blk) return -1;
+    if (m < 1 || m > 200 || n % blk) return -1;
     if (k < 0 || (k > 0 && (nb <= 0 || n % nb || !v || !wt))) return -1;
 
-    int8_t pal[28 * 28];
-    nar_oracle_paley(m, pal);
+    int8_t *pal = (int8_t *)malloc((size_t)m * (size_t)m);
+    if (!pal) return -1;
+    if (nar_oracle_paley(m, pal)) { free(pal); return -1; }
     const float sq = (float)sqrt((double)q);
-    const float hm = 1.0f / (float)sqrt((double)m);   /* |entry| of H_m / sqrt(m) */
+    /* |entry| of H_m / sqrt(m): fp32(1) / fp32(sqrt(m)) as the reference's fp32
+     * factors (12, 28; for 20 and 76 equal to RN32 of the fp64 1/sqrt(m) that
+     * paley_hadamard casts); the fp64 value for 68 and 200, whose product the
+     * reference forms in fp64 (nar/activation_experiments.py:205-215) */
+    const double hm = (m == 68 || m == 200) ? 1.0 / sqrt((double)m) : (double)(1.0f / (float)sqrt((double)m));
 
     float *row = (float *)malloc(sizeof(float) * (size_t)n);
     float *pr = (float *)malloc(sizeof(float) * (size_t)n);
     float *u = (float *)malloc(sizeof(float) * (size_t)(k > 0 ? (n / nb) * k : 1));
-    if (!row || !pr || !u) { free(row); free(pr); free(u); return -1; }
+    if (!row || !pr || !u) { free(row); free(pr); free(u); free(pal); return -1; }
 
     for (int64_t t = 0; t < T; t++) {
         const float *xt = x + t * ldx;
@@ -218,7 +271,7 @@ int nar_oracle_rotate(const float *x, int64_t T, int64_t n, int64_t ldx,
                     for (int c = 0; c < q; c++) {
                         double acc = 0.0;
                         for (int a2 = 0; a2 < m; a2++) {
-                            float h = pal[a * m + a2] > 0 ? hm : -hm;
+                            double h = pal[a * m + a2] > 0 ? hm : -hm;
                             acc += (double)row[b0 + (int64_t)a2 * q + c] * (double)h;
                         }
                         pr[b0 + (int64_t)a * q + c] = (float)acc;
@@ -246,7 +299,7 @@ int nar_oracle_rotate(const float *x, int64_t T, int64_t n, int64_t ldx,
             memcpy(out + t * ldo, pr, sizeof(float) * (size_t)n);
         }
     }
-    free(row); free(pr); free(u);
+    free(row); free(pr); free(u); free(pal);
     return 0;
 }
 

@@ -30,7 +30,7 @@ def test_library_exports_every_declared_symbol():
     assert lib.narhip_abi_version() == 1
 
 
-@pytest.mark.parametrize("m", [12, 28])
+@pytest.mark.parametrize("m", [12, 20, 28])
 def test_library_paley_equals_oracle(m):
     import narhip
     out = np.zeros((m, m), np.int8)
@@ -40,10 +40,10 @@ def test_library_paley_equals_oracle(m):
 
 def test_unsupported_paley_order():
     import narhip
-    out = np.zeros((20, 20), np.int8)
+    out = np.zeros((24, 24), np.int8)
     lib = narhip.load()
-    assert lib.narhip_paley(20, out.ctypes.data_as(ctypes.c_void_p)) == -2
-    assert b"20" in lib.narhip_last_error_string()
+    assert lib.narhip_paley(24, out.ctypes.data_as(ctypes.c_void_p)) == -2
+    assert b"24" in lib.narhip_last_error_string()
 
 
 def _rq(lib, **kw):
@@ -58,7 +58,10 @@ def _rq(lib, **kw):
     (dict(n=1000), -1),                       # n % 128
     (dict(q=96), -2),                         # not a power of two
     (dict(q=2048), -2),                       # beyond the built widths
-    (dict(m=20, q=128, n=2560), -2),          # no Paley 20
+    (dict(m=24, q=128, n=3072), -2),          # no Paley 24
+    (dict(m=68, q=256, n=17408), -2),         # Qwen3 order 68: not built
+    (dict(q=4096, n=4096, ld=4096, k=8, v=16, wt=16), -2),   # no rank term on the full-row FWHT
+    (dict(q=16384, n=16384, ld=16384), -2),   # FWHT rows beyond 8192
     (dict(group=48), -2),
     (dict(k=65, wt=1), -2),
     (dict(m=28, q=512, n=14336, ld=14336, k=32, nb=14336, v=16, wt=16, x=16, codes=16, scales=16, zeros=16), -4),
