@@ -202,7 +202,7 @@ int narhip_hadamard_rows(const void *x_bf16, int64_t rows, int64_t n, int64_t ld
 
 /* E28's down_proj transform, fp16 in and fp16 out, no quantization:
  * out = fp16( H_q-blocks(x) / fp32(sqrt q) - RN32(u W^T) ) per row of x fp16
- * [tokens, ld_x], q in {128, ..., 1024} (E28: 128), w_t fp32 [k, n], k <= 16.
+ * [tokens, ld_x], q in {128, ..., 1024} (E28: 128), w_t fp32 [k, n], k <= 64.
  * u comes from `partial` fp32 [tokens, splits*k] (the split partials of
  * narhip_rank_projection_f16, folded in split order; Kernel B alone) or, with
  * partial NULL, is computed here from v fp32 [n, k] (u = RN32(x V), fp64
@@ -218,7 +218,7 @@ size_t narhip_transform_f16_workspace(int64_t tokens, int64_t n, int32_t k);
 
 /* Kernel A of the E28 transform on fp16 rows: partial[t, s*k + r] =
  * RN32(sum over channel split s of x[t, i] v[i, r]) with fp64 sums, v fp32
- * [n, k], 1 <= k <= 16, n / splits even.  Replaces launch_projection_dot on fp16
+ * [n, k], 1 <= k <= 64, n / splits even.  Replaces launch_projection_dot on fp16
  * input with TERMS = 2 fp16 factor terms (quarot-llama3/nar_r4_kernel.py:272,
  * nar/kernels/r4_fused_v3.py:187-201). */
 int narhip_rank_projection_f16(const void *x_f16, int64_t tokens, int64_t n, int64_t ld_x, const float *v,

@@ -745,7 +745,7 @@ int narhip_hadamard_rows(const void *x_bf16, int64_t rows, int64_t n, int64_t ld
 
 size_t narhip_transform_f16_workspace(int64_t tokens, int64_t n, int32_t k)
 {
-    if (tokens <= 0 || n <= 0 || k <= 0 || k > 16) return 0;
+    if (tokens <= 0 || n <= 0 || k <= 0 || k > 64) return 0;
     size_t fast = 0;
     if (k <= XF_K && n % 128 == 0)
         fast = xf_pd_bytes(tokens, xf_splits(tokens, n));
@@ -760,7 +760,7 @@ int narhip_rank_projection_f16(const void *x_f16, int64_t tokens, int64_t n, int
 {
     clear_error();
     if (tokens < 0 || n <= 0 || ld_x < n || ld_x % 8) return fail(NARHIP_EINVAL, "bad shape");
-    if (k < 1 || k > 16) return fail(NARHIP_EUNSUPPORTED, "fp16 projection supports rank k in [1, 16] (got %d)", k);
+    if (k < 1 || k > 64) return fail(NARHIP_EUNSUPPORTED, "fp16 projection supports rank k in [1, 64] (got %d)", k);
     if (splits < 1 || n % splits || (n / splits) % 2)
         return fail(NARHIP_EINVAL, "%lld channels do not divide into %d even splits", (long long)n, splits);
     if (tokens == 0) return NARHIP_OK;
@@ -779,7 +779,7 @@ int narhip_transform_f16(const void *x_f16, int64_t tokens, int64_t n, int64_t l
     if (!pow2(had_q) || had_q < 128 || had_q > 1024 || n % had_q)
         return fail(NARHIP_EUNSUPPORTED, "block Hadamard width %d must be a power of two in [128, 1024] dividing n",
                     had_q);
-    if (k < 0 || k > 16) return fail(NARHIP_EUNSUPPORTED, "fp16 transform supports rank k <= 16 (got %d)", k);
+    if (k < 0 || k > 64) return fail(NARHIP_EUNSUPPORTED, "fp16 transform supports rank k <= 64 (got %d)", k);
     if (ld_x < n || ld_x % 8) return fail(NARHIP_EINVAL, "ld_x=%lld must be >= n and a multiple of 8", (long long)ld_x);
     if (partial && (splits < 1 || k < 1)) return fail(NARHIP_EINVAL, "partials need splits >= 1 and k >= 1");
     if (tokens == 0) return NARHIP_OK;

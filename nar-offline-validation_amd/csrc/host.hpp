@@ -92,7 +92,8 @@ inline int f64_splits(int64_t T, int64_t n)
     while (s < 64 && tiles * s * 2 <= 1024 && n % (128 * 2 * (int64_t)s) == 0) s *= 2;
     return s;
 }
-inline int f64_kmax(int k) { return k <= 8 ? 8 : 16; }
+// rank stride of the fp64 partials: 8, else k rounded up to slices of 16
+inline int f64_kmax(int k) { return k <= 8 ? 8 : round_up(k, 16); }
 
 // Channel splits for the MFMA projection: enough workgroups for two per CU
 // (128-token tiles, splits of a multiple of 128 channels).

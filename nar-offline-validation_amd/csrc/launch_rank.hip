@@ -45,16 +45,21 @@ int launch_proj_f64(const uint16_t *x, int64_t T, int64_t n, int64_t ldx, const 
                     double *pd, hipStream_t s, bool f16, float *pf)
 {
     if (T == 0) return NARHIP_OK;
-    ProjF64Args a{x, ldx, T, n, v, pd, k, splits, pf};
+    ProjF64Args a{x, ldx, T, n, v, pd, k, splits, pf, 0, f64_kmax(k)};
     dim3 grid((unsigned)((T + 15) / 16), (unsigned)splits);
-    if (f16) {
-        if (k <= 8) hipLaunchKernelGGL((proj_f64_kernel<8, true>), grid, dim3(256), 0, s, a);
-        else hipLaunchKernelGGL((proj_f64_kernel<16, true>), grid, dim3(256), 0, s, a);
-    } else {
-        if (k <= 8) hipLaunchKernelGGL((proj_f64_kernel<8>), grid, dim3(256), 0, s, a);
-        else hipLaunchKernelGGL((proj_f64_kernel<16>), grid, dim3(256), 0, s, a);
+    // k > 16: one launch per slice of 16 ranks (each an fp64 sum per rank, so
+    // the slicing does not change any partial)
+    for (a.r0 = 0; a.r0 < k; a.r0 += 16) {
+        if (f16) {
+            if (k <= 8) hipLaunchKernelGGL((proj_f64_kernel<8, true>), grid, dim3(256), 0, s, a);
+            else hipLaunchKernelGGL((proj_f64_kernel<16, true>), grid, dim3(256), 0, s, a);
+        } else {
+            if (k <= 8) hipLaunchKernelGGL((proj_f64_kernel<8>), grid, dim3(256), 0, s, a);
+            else hipLaunchKernelGGL((proj_f64_kernel<16>), grid, dim3(256), 0, s, a);
+        }
+        if (int rc = check_launch("proj_f64_kernel")) return rc;
     }
-    return check_launch("proj_f64_kernel");
+    return NARHIP_OK;
 }
 
 int launch_fold_f64(const double *pd, int splits, int kmax, int k, int64_t T, float *u, hipStream_t s)

@@ -86,7 +86,8 @@ int launch_seg_f16(const SegArgs &a, int q, int k, hipStream_t s)
     dim3 grid((unsigned)((segs + 15) / 16));
     if (grid.x == 0) return NARHIP_OK;
 #define NARHIP_F16_SEG(QQ)                                                                                      \
-    if (k > 0) hipLaunchKernelGGL((rq_seg_kernel<QQ, 128, RANK_PARTIAL, 16, true>), grid, dim3(256), 0, s, a); \
+    if (k > 16) hipLaunchKernelGGL((rq_seg_kernel<QQ, 128, RANK_PARTIAL, 64, true>), grid, dim3(256), 0, s, a); \
+    else if (k > 0) hipLaunchKernelGGL((rq_seg_kernel<QQ, 128, RANK_PARTIAL, 16, true>), grid, dim3(256), 0, s, a); \
     else hipLaunchKernelGGL((rq_seg_kernel<QQ, 128, RANK_NONE, 0, true>), grid, dim3(256), 0, s, a);
     switch (q) {
     case 128: NARHIP_F16_SEG(128) break;

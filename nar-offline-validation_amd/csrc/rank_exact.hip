@@ -92,9 +92,11 @@ struct ProjF64Args {
     const uint16_t *x;      // bf16 or (F16) fp16 rows
     int64_t ldx, T, n;
     const float *v;         // [n, k]
-    double *pd;             // [T][splits][KMAX], or null when pf is set
+    double *pd;             // [T][splits][kstride], or null when pf is set
     int k, splits;
     float *pf;              // null, or fp32 partials [T, splits*k] (each split rounded once)
+    int r0;                 // first rank of this launch's slice of KMAX ranks
+    int kstride;            // rank stride of pd (>= k, a multiple of KMAX)
 };
 
 __device__ __forceinline__ double wave_sum64(double v)
@@ -132,7 +134,7 @@ proj_f64_kernel(ProjF64Args a)
         for (int r = 0; r < KMAX; r++) acc[tt][r] = 0.0;
     for (int64_t c = c_begin + 2 * lane; c < c_end; c += 128) {
         double v0[KMAX], v1[KMAX];
-        if (a.k == KMAX) {
+        if (a.k == KMAX && a.r0 == 0) {
             // rows c and c+1 of V: 2 KMAX contiguous floats, 32-byte aligned
             const float4 *vr = reinterpret_cast<const float4 *>(a.v + c * KMAX);
 #pragma unroll
@@ -144,8 +146,9 @@ proj_f64_kernel(ProjF64Args a)
         } else {
 #pragma unroll
             for (int r = 0; r < KMAX; r++) {
-                v0[r] = r < a.k ? (double)a.v[c * a.k + r] : 0.0;
-                v1[r] = r < a.k ? (double)a.v[(c + 1) * a.k + r] : 0.0;
+                const int rr = a.r0 + r;
+                v0[r] = rr < a.k ? (double)a.v[c * a.k + rr] : 0.0;
+                v1[r] = rr < a.k ? (double)a.v[(c + 1) * a.k + rr] : 0.0;
             }
         }
 #pragma unroll
@@ -165,9 +168,9 @@ proj_f64_kernel(ProjF64Args a)
             const double sum = wave_sum64(acc[tt][r]);
             if (lane == 0 && t < a.T) {
                 if (a.pf) {
-                    if (r < a.k) a.pf[(t * a.splits + split) * a.k + r] = (float)sum;
+                    if (a.r0 + r < a.k) a.pf[(t * a.splits + split) * a.k + a.r0 + r] = (float)sum;
                 } else {
-                    a.pd[(t * a.splits + split) * KMAX + r] = sum;
+                    a.pd[(t * a.splits + split) * a.kstride + a.r0 + r] = sum;
                 }
             }
         }

@@ -111,7 +111,7 @@ def _tf(lib, **kw):
     (dict(q=96), -2),                               # not a power of two
     (dict(q=2048), -2),
     (dict(n=8064, ld=8064, q=256), -2),             # 256 does not divide n
-    (dict(k=17, wt=16, v=16), -2),                  # rank beyond the fp16 path
+    (dict(k=65, wt=16, v=16), -2),                  # rank beyond the fp16 path
     (dict(ld=8190), -1),
     (dict(k=8, wt=16, partial=16, splits=0), -1),   # partials without splits
     (dict(k=8, wt=16, v=16, x=16, out=16), -4),     # projection workspace missing
@@ -128,13 +128,15 @@ def test_transform_f16_workspace_query():
     import narhip
     lib = narhip.load()
     assert lib.narhip_transform_f16_workspace(2048, 14336, 0) == 0
-    assert lib.narhip_transform_f16_workspace(2048, 14336, 17) == 0
+    assert lib.narhip_transform_f16_workspace(2048, 14336, 65) == 0
+    # k = 32: fp64 partials in two slices of 16 ranks, plus u
+    assert lib.narhip_transform_f16_workspace(2048, 14336, 32) >= 2048 * 32 * (8 + 4)
     ws = lib.narhip_transform_f16_workspace(2048, 14336, 8)
     assert ws >= 2048 * 8 * 4 + 2048 * 8 * 8 and ws % 256 == 0
 
 
 @pytest.mark.parametrize("k,n,splits,code", [
-    (0, 14336, 1, -2), (17, 14336, 1, -2),
+    (0, 14336, 1, -2), (65, 14336, 1, -2),
     (8, 14336, 3, -1),          # 3 does not divide n
     (8, 14343, 7, -1),          # 7 x 2049: odd channel chunks
 ])

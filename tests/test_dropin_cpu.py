@@ -101,6 +101,6 @@ def test_e28_module_host_logic():
     with pytest.raises(ValueError):
         mod(torch.zeros((2, n), dtype=torch.float16))          # host tensor
     with pytest.raises(ValueError):
-        nk.NARDownTransform(torch.zeros((n, 20)), torch.zeros((20, n)), 20, sel)
+        nk.NARDownTransform(torch.zeros((n, 72)), torch.zeros((72, n)), 72, sel)
     with pytest.raises(ValueError):
         nk.NARDownTransform(y, w[:, :512], k, sel)

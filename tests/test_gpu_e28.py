@@ -195,9 +195,10 @@ def test_select_configs_then_module():
     assert worst <= 1
 
 
-@pytest.mark.parametrize("k,q", [(12, 128), (16, 128), (8, 256), (4, 1024)])
+@pytest.mark.parametrize("k,q", [(12, 128), (16, 128), (8, 256), (4, 1024), (32, 128), (24, 128), (64, 256)])
 def test_transform_segment_kernel_forms(k, q):
-    """Ranks 9..16 and Hadamard blocks wider than 128 run on the segment kernel's fp16 form."""
+    """Ranks 9..64 and Hadamard blocks wider than 128 run on the segment kernel's fp16
+    form (ranks above 16: the fp64 projection in slices of 16 ranks)."""
     print(f"[test_transform_segment_kernel_forms] k={k} q={q}", flush=True)
     n = 8192
     y, w = factors(n, k=k, seed=k + q)
@@ -208,3 +209,35 @@ def test_transform_segment_kernel_forms(k, q):
     worst, frac = f16_ulp_report(out, ref)
     print(f"  max ulp {worst}, differing fraction {frac:.2e}", flush=True)
     assert worst <= 1 and frac <= 1e-4
+
+
+@pytest.mark.parametrize("k", [32, 20])
+def test_module_with_e17_rank(k):
+    """NARDownTransform at ranks above 16 -- E17's k = 32 factors (the reference
+    pads the rank with no cap, quarot-llama3/nar_r4_kernel.py:178-187,225-243):
+    forward against the oracle and E28's acceptance, and the Kernel A -> Kernel B
+    sequence on the fp16 factor terms against the factors those terms carry."""
+    print(f"[test_module_with_e17_rank] k={k}", flush=True)
+    n, t = 14336, 120
+    y, w = factors(n, k=k, seed=5 + k)
+    x = rows(t, n, seed=k).cuda()
+    mod = nk.NARDownTransform(torch.from_numpy(y), torch.from_numpy(w), k, {}).cuda()
+    out = mod(x)
+    torch.cuda.synchronize()
+    worst, frac = f16_ulp_report(out, O.rotate(x.float().cpu().numpy(), 1, 128, v=y, wt=w))
+    print(f"  forward: max ulp {worst}, differing fraction {frac:.2e}", flush=True)
+    assert worst <= 1 and frac <= 1e-4
+    e28_accept(out, x.cpu(), y, w)
+    y_t = (mod.y_terms.reshape(2, n, -1)[:, :, :k].float().sum(0)).cpu().numpy()
+    w_t = (mod.w_hi.float() + mod.w_lo.float()).cpu().numpy()
+    ref = O.rotate(x.float().cpu().numpy(), 1, 128, v=y_t, wt=w_t)
+    for splits in (1, 4):
+        proj = k3.ProjectionConfig(32, 128, splits, 8, 3)
+        partial = torch.empty((t, splits * k), dtype=torch.float32, device="cuda")
+        k3.launch_projection_dot(x, mod.y_terms, partial, k, proj, nk.TERMS)
+        out_b = torch.empty_like(x)
+        nk.launch_kernel_b(x, partial, None, out_b, k, nk.REFERENCE_TILE, mod.h128, mod.w_hi, mod.w_lo)
+        torch.cuda.synchronize()
+        worst, frac = f16_ulp_report(out_b, ref)
+        print(f"  A(splits={splits}) -> B: max ulp {worst}, differing fraction {frac:.2e}", flush=True)
+        assert worst <= 1 and frac <= 1e-3
