@@ -15,7 +15,12 @@ int launch_seg_qb(const SegArgs &a, int mode, hipStream_t s)
     if (grid.x == 0) return NARHIP_OK;
     switch (mode) {
     case RANK_NONE: hipLaunchKernelGGL((rq_seg_kernel<Q, B, RANK_NONE, 0>), grid, dim3(256), 0, s, a); break;
-    case RANK_LOCAL: hipLaunchKernelGGL((rq_seg_kernel<Q, B, RANK_LOCAL, 8>), grid, dim3(256), 0, s, a); break;
+    case RANK_LOCAL:
+        // per-block rank, compiled for the rank (KV heads: k = 2 or 4)
+        if (a.k <= 2) hipLaunchKernelGGL((rq_seg_kernel<Q, B, RANK_LOCAL, 2>), grid, dim3(256), 0, s, a);
+        else if (a.k <= 4) hipLaunchKernelGGL((rq_seg_kernel<Q, B, RANK_LOCAL, 4>), grid, dim3(256), 0, s, a);
+        else hipLaunchKernelGGL((rq_seg_kernel<Q, B, RANK_LOCAL, 8>), grid, dim3(256), 0, s, a);
+        break;
     default:
         if (a.k <= 16) hipLaunchKernelGGL((rq_seg_kernel<Q, B, RANK_PARTIAL, 16>), grid, dim3(256), 0, s, a);
         else hipLaunchKernelGGL((rq_seg_kernel<Q, B, RANK_PARTIAL, 64>), grid, dim3(256), 0, s, a);

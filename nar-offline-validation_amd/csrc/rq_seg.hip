@@ -76,9 +76,54 @@ rq_seg_kernel(SegArgs a)
         }
     }
 
+    // ---- per-head rank (one 128-channel block per row): the V rows of the
+    // lane's 8 channels, the W rows over them and the destination row are
+    // requested together with x, so the row waits on memory once (the decode
+    // and KV-cache shapes are latency-bound)
+    constexpr bool HEAD = MODE == RANK_LOCAL && NH == 1;
+    float vh[HEAD ? 8 * KMAX : 1], wh[HEAD ? 8 * KMAX : 1];
+    if constexpr (HEAD) {
+        const int64_t c0 = base + chunk * 8;
+        if (a.k == KMAX && (reinterpret_cast<uintptr_t>(a.v) & 15u) == 0) {
+            const float4 *vr = reinterpret_cast<const float4 *>(a.v + c0 * KMAX);
+#pragma unroll
+            for (int q4 = 0; q4 < 2 * KMAX; q4++) {
+                const float4 f = vr[q4];
+                vh[4 * q4] = f.x; vh[4 * q4 + 1] = f.y; vh[4 * q4 + 2] = f.z; vh[4 * q4 + 3] = f.w;
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; e++)
+#pragma unroll
+                for (int r = 0; r < KMAX; r++) vh[e * KMAX + r] = r < a.k ? a.v[(c0 + e) * a.k + r] : 0.0f;
+        }
+#pragma unroll
+        for (int r = 0; r < KMAX; r++) {
+            const int rr = r < a.k ? r : 0;   // rows r >= k are loaded but never used
+            const float4 *wr = reinterpret_cast<const float4 *>(a.wt + (int64_t)rr * a.n + c0);
+            const float4 w0 = wr[0], w1 = wr[1];
+            wh[r * 8 + 0] = w0.x; wh[r * 8 + 1] = w0.y; wh[r * 8 + 2] = w0.z; wh[r * 8 + 3] = w0.w;
+            wh[r * 8 + 4] = w1.x; wh[r * 8 + 5] = w1.y; wh[r * 8 + 6] = w1.z; wh[r * 8 + 7] = w1.w;
+        }
+    }
+    const int64_t orow = a.dest ? a.dest[t] : t;
+
     // ---- rank-k projection of the raw input (fp64, rounded once to fp32)
     float u[KMAX > 0 ? KMAX : 1];
-    if constexpr (MODE == RANK_LOCAL) {
+    if constexpr (HEAD) {
+        double acc[KMAX];
+#pragma unroll
+        for (int r = 0; r < KMAX; r++) acc[r] = 0.0;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const double xv = (double)v[e];
+#pragma unroll
+            for (int r = 0; r < KMAX; r++)
+                if (r < a.k) acc[r] = fma(xv, (double)vh[e * KMAX + r], acc[r]);
+        }
+#pragma unroll
+        for (int r = 0; r < KMAX; r++) u[r] = (float)row_sum64(acc[r]);
+    } else if constexpr (MODE == RANK_LOCAL) {
         double acc[KMAX];
 #pragma unroll
         for (int r = 0; r < KMAX; r++) acc[r] = 0.0;
@@ -119,7 +164,21 @@ rq_seg_kernel(SegArgs a)
     div_sqrt_q<Q>(v, a.sq, a.rsq);
 
     // ---- rank-k correction: x' = Hx - RN32(sum_r u_r W[r, i])
-    if constexpr (MODE != RANK_NONE) {
+    if constexpr (HEAD) {
+        double acc[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) acc[e] = 0.0;
+#pragma unroll
+        for (int r = 0; r < KMAX; r++) {
+            if (r < a.k) {
+                const double ur = (double)u[r];
+#pragma unroll
+                for (int e = 0; e < 8; e++) acc[e] = fma(ur, (double)wh[r * 8 + e], acc[e]);
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < 8; e++) v[e] = v[e] - (float)acc[e];
+    } else if constexpr (MODE != RANK_NONE) {
         // per channel: fp64 sum over r in order, rounded once; W rows read as float4
 #pragma unroll
         for (int h = 0; h < NH; h++) {
@@ -172,7 +231,6 @@ rq_seg_kernel(SegArgs a)
     // ---- quantize groups of B and store (codes == null: rotation only, into
     // `rotated`; deq set: the hooks' tuple, codes unpacked)
     if (!a.codes) return;
-    const int64_t orow = a.dest ? a.dest[t] : t;
     const int64_t gpt = a.n / B;   // groups per token
 #pragma unroll
     for (int h = 0; h < NH; h++) {
