@@ -17,7 +17,9 @@ from __future__ import annotations
 
 import argparse
 import json
+import ctypes
 import os
+import re
 import statistics
 import sys
 import time
@@ -32,29 +34,58 @@ METRIC = "fused NAR+INT4 quant: tokens/s and achieved HBM GB/s (% peak), 1 MI355
 HBM_PEAK_GBPS = 8000.0
 MALL_BYTES = 256 << 20
 
-# HBM bytes per call of the default (auto) path, summed over its dispatches:
-# rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE (KiB per dispatch) on bench.py,
-# FETCH_SIZE scaled by 2.0 and WRITE_SIZE by 1.0 -- the factors that make the
-# counters read a 1 GiB device copy (bench.py --copy-mb 1024) as 1 GiB each way.
-TRAFFIC_SOURCE = "profiles/hbm_traffic.md"
-# MFMA busy fraction of the rank-k kernels (SQ_VALU_MFMA_BUSY_CYCLES over 1024 SIMDs x the kernel's
-# cycles, profiles/mfma_utilisation.md), for the workloads on the MFMA rank path.
-MFMA_UTIL_SOURCE = "profiles/mfma_utilisation.md"
-MFMA_UTIL = {
-    "qproj_3b": {"proj_mfma": 0.028, "corr_quant": 0.065},
-    "downproj_8b": {"proj_mfma": 0.145, "corr_quant": 0.138},
-    "downproj_70b": {"proj_mfma": 0.337, "corr_quant": 0.295},
-}
-TRAFFIC_BYTES = {
-    "downproj_8b": 1570.5e6,
-    "downproj_70b": 6283.5e6,
-    "qproj_3b": 171.5e6,
-    "kcache_3b": 5.8e6,
-    "vcache_decode_8b": 0.6e6,
-    "e17_8b_k8": 152.7e6,
-    "e28_8b_2048": 195.6e6,
-    "e28_8b_32768": 2896.1e6,
-}
+# HBM bytes per call and MFMA busy fractions are measured with rocprofv3 counter
+# runs of this script (the commands are in the profiles) and filed under the
+# SHA-256 of the kernel sources they were taken on; a profile of other sources
+# is reported as stale (null), never as a number for the current kernels.
+TRAFFIC_SOURCE = ROOT / "profiles" / "hbm_traffic.md"
+MFMA_UTIL_SOURCE = ROOT / "profiles" / "mfma_utilisation.md"
+
+
+def _profile_sections(path: Path) -> dict[str, str]:
+    """'## <config> ...' sections of a profile, keyed by config name."""
+    if not path.exists():
+        return {}
+    out, cur = {}, None
+    for line in path.read_text().splitlines():
+        if line.startswith("## "):
+            cur = line[3:].split()[0]
+            out[cur] = ""
+        elif cur:
+            out[cur] += line + "\n"
+    return out
+
+
+def _sources_key(text: str) -> str | None:
+    m = re.search(r"Kernel sources sha256: ([0-9a-f]{64})", text)
+    return m.group(1) if m else None
+
+
+def measured_traffic(config: str, sha: str) -> tuple[float | None, str]:
+    """(HBM bytes per call, status) from the traffic profile of this config."""
+    sec = _profile_sections(TRAFFIC_SOURCE).get(config)
+    if sec is None:
+        return None, "not profiled"
+    if _sources_key(sec) != sha:
+        return None, "stale: profiled on other kernel sources"
+    m = re.search(r"Total per call: \*\*([0-9.]+) MB\*\*", sec)
+    return (float(m.group(1)) * 1e6, "measured") if m else (None, "no total")
+
+
+def measured_mfma_busy(config: str, sha: str) -> dict | None:
+    """MFMA busy fraction per kernel of this config, or None if not profiled on these sources."""
+    if not MFMA_UTIL_SOURCE.exists():
+        return None
+    text = MFMA_UTIL_SOURCE.read_text()
+    if _sources_key(text) != sha:
+        return None
+    busy = {}
+    for line in text.splitlines():
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if len(cells) >= 4 and cells[0] == config and cells[3].endswith("%"):
+            kernel = re.sub(r"[`<].*", "", cells[1].replace("void ", "").strip("` ")) or cells[1]
+            busy[kernel] = float(cells[3].rstrip("%")) / 100.0
+    return busy or None
 
 
 def parse() -> argparse.Namespace:
@@ -70,6 +101,8 @@ def parse() -> argparse.Namespace:
                     help="token count of the e28_* transform settings (default 2048) and of w4a4_8b "
                          "(default 8192)")
     ap.add_argument("--rank-mode", default="auto", choices=["auto", "exact", "mfma"])
+    ap.add_argument("--api", default="cabi", choices=["cabi", "op"],
+                    help="time the C-ABI entry point (default) or the torch.ops.narhip operator")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU baseline work")
     ap.add_argument("--copy-mb", type=int, default=0,
@@ -155,7 +188,8 @@ def main() -> int:
     import numpy as np
     import torch
 
-    from narhip import ops, workloads
+    from narhip import _lib, ops, workloads
+    from narhip.build import sources_sha256
 
     mode = {"auto": ops.RANK_AUTO, "exact": ops.RANK_EXACT, "mfma": ops.RANK_MFMA}[args.rank_mode]
     if args.config == "w4a4_8b":
@@ -182,10 +216,29 @@ def main() -> int:
     # factor terms are prepared once per factor set, as the reference's modules do
     prepared = ops.prepare_rank_factors(v, wt, w.n, w.k) if full_row_rank and mode != ops.RANK_EXACT else None
 
+    # The timed step calls the C ABI (include/narhip.h) directly: the drop-in
+    # boundary of the path.  The torch.ops.narhip operator over the same entry
+    # point adds 25-35 us of Python dispatch per call (--api op times that).
+    lib = _lib.load()
+    m, q = w.hadamard
+    nb = w.n if w.rank_block is None else w.rank_block
+    ws_bytes = lib.narhip_rotate_quant_workspace(w.tokens, w.n, m, q, w.k, nb, 0, 0, int(prepared is not None),
+                                                 mode)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    p = lambda t: None if t is None else ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    cstream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
     def step(i: int) -> None:
         c, s, z = outs[i % R]
-        ops.rotate_quant(xs[i % R], hadamard=w.hadamard, v=v, w_t=wt, prepared=prepared, rank_block=w.rank_block,
-                         group=w.group, codes=c, scales=s, zeros=z, dest_rows=dest, rank_mode=mode)
+        if args.api == "op":
+            ops.rotate_quant(xs[i % R], hadamard=w.hadamard, v=v, w_t=wt, prepared=prepared,
+                             rank_block=w.rank_block, group=w.group, codes=c, scales=s, zeros=z, dest_rows=dest,
+                             rank_mode=mode)
+            return
+        rc = lib.narhip_rotate_quant(p(xs[i % R]), w.tokens, w.n, w.n, m, q, None, w.k, nb, p(v), p(wt), p(prepared),
+                                     None, 0, w.group, p(c), p(s), p(z), None, p(dest), mode, p(ws), ws_bytes,
+                                     cstream)
+        _lib.check(rc)
 
     for i in range(args.warmup):
         step(i)
@@ -220,7 +273,8 @@ def main() -> int:
         kernels = "proj_exact + corr_exact + rq_row" if kron else "proj_exact + rq_seg"
     else:
         kernels = "kron_mfma" if kron else "rq_seg"
-    traffic = TRAFFIC_BYTES.get(args.config) if mode == ops.RANK_AUTO else None
+    sha = sources_sha256()
+    traffic, traffic_status = measured_traffic(args.config, sha) if mode == ops.RANK_AUTO else (None, "auto only")
     line = {
         "metric": METRIC,
         "value": t / (ms_step * 1e-3),
@@ -241,10 +295,14 @@ def main() -> int:
         "wall_s": wall,
         "roofline": {"kernel": f"rotate_quant call ({kernels})", "bound": "hbm", "achieved": achieved,
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBPS,
-                     "traffic": traffic, "traffic_source": TRAFFIC_SOURCE if traffic else None},
+                     "traffic": traffic, "traffic_source": "profiles/hbm_traffic.md" if traffic else None,
+                     "traffic_status": traffic_status},
+        "kernel_sources_sha256": sha,
+        "api": args.api,
     }
-    if args.config in MFMA_UTIL and mode == ops.RANK_AUTO:
-        line["rank_stage_mfma_busy"] = dict(MFMA_UTIL[args.config], source=MFMA_UTIL_SOURCE)
+    busy = measured_mfma_busy(args.config, sha) if mode == ops.RANK_AUTO else None
+    if busy:
+        line["rank_stage_mfma_busy"] = dict(busy, source="profiles/mfma_utilisation.md")
     if w.dest_rows is not None:
         line["us_per_call"] = ms_step * 1e3
     if not args.no_cpu_baseline:
@@ -285,7 +343,9 @@ def bench_transform_f16(args, w, dev) -> int:
     t, n = w.tokens, w.n
     alg_bytes = w.algorithmic_bytes()
     achieved = alg_bytes / (ms_step * 1e-3) / 1e9
-    traffic = TRAFFIC_BYTES.get(f"{args.config}_{t}")
+    from narhip.build import sources_sha256
+    sha = sources_sha256()
+    traffic, traffic_status = measured_traffic(f"{args.config}_{t}", sha)
     line = {
         "metric": "E28 fp16 down_proj transform (NARDownTransform.forward): tokens/s, 1 MI355X",
         "value": t / (ms_step * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
@@ -298,7 +358,9 @@ def bench_transform_f16(args, w, dev) -> int:
         "roofline": {"kernel": "transform_f16 call (proj_tok + xform128)", "bound": "hbm",
                      "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBPS, "traffic": traffic,
-                     "traffic_source": TRAFFIC_SOURCE if traffic else None},
+                     "traffic_source": "profiles/hbm_traffic.md" if traffic else None,
+                     "traffic_status": traffic_status},
+        "kernel_sources_sha256": sha,
     }
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline_transform(w, args.cpu_seconds)

@@ -46,6 +46,17 @@ FLAGS = [
 ]
 
 
+def sources_sha256() -> str:
+    """SHA-256 over the kernel and ABI sources (csrc/*.hip, csrc/*.hpp, include/narhip.h, by name): the
+    key under which measured profiles (HBM traffic, MFMA utilisation) are filed, so that a profile taken
+    on other kernels is recognised as stale."""
+    import hashlib
+    h = hashlib.sha256()
+    for p in SOURCES + [ROOT.parent / "include" / "narhip.h"]:
+        h.update(p.name.encode() + b"\0" + p.read_bytes() + b"\0")
+    return h.hexdigest()
+
+
 def hipcc() -> str:
     rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
     cand = Path(rocm) / "bin" / "hipcc"
