@@ -96,7 +96,7 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--config", default="downproj_8b",
                     choices=["kcache_3b", "qproj_3b", "downproj_8b", "vcache_decode_8b", "downproj_70b",
                              "e17_8b_k8", "e17_8b_k32", "e17_3b_k8", "e17_3b_k32", "e28_8b", "e28_3b",
-                             "w4a4_8b"])
+                             "w4a4_8b", "hook_kcache_3b", "hook_rows_8192"])
     ap.add_argument("--tokens", type=int, default=0,
                     help="token count of the e28_* transform settings (default 2048) and of w4a4_8b "
                          "(default 8192)")
@@ -192,6 +192,8 @@ def main() -> int:
     from narhip.build import sources_sha256
 
     mode = {"auto": ops.RANK_AUTO, "exact": ops.RANK_EXACT, "mfma": ops.RANK_MFMA}[args.rank_mode]
+    if args.config.startswith("hook_"):
+        return bench_hook(args, torch.device("cuda:0"))
     if args.config == "w4a4_8b":
         return bench_w4a4(args, torch.device("cuda:0"))
     if args.config.startswith("e28_"):
@@ -364,6 +366,75 @@ def bench_transform_f16(args, w, dev) -> int:
     }
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline_transform(w, args.cpu_seconds)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def bench_hook(args, dev) -> int:
+    """The fused hook call (rotate, dynamic_asym_int4, dequantize; one kernel) through the C ABI:
+    hook_kcache_3b -- the K-cache shape (2048 x 8 heads x 128 bf16, H_128 and rank 2 per head, b = 32);
+    hook_rows_8192 -- 4096 rows of 8192 bf16 (full-row FWHT, the Llama-3.2-3B down_proj width, b = 128)."""
+    import numpy as np
+    import torch
+
+    from narhip import _lib, workloads
+    if args.config == "hook_kcache_3b":
+        w = workloads.kcache_3b(args.tokens or 2048)
+        m, q, nb = 1, 128, 128
+        desc = f"hook_kcache_3b: {w.tokens} x 8 heads x 128 bf16, H128 + rank 2 per head, b=32, tuple out"
+    else:
+        T, n = args.tokens or 4096, 8192
+        rng = np.random.default_rng(20260902)
+        x = rng.standard_normal((T, n), dtype=np.float32)
+        w = workloads.Workload("hook_rows_8192", workloads.bf16_bits(x), (1, n), 128)
+        m, q, nb = 1, n, n
+        desc = f"hook_rows_8192: {T} x {n} bf16, full-row FWHT, b=128, tuple out"
+    T, n, b = w.tokens, w.n, w.group
+    k = w.k
+    x = torch.from_numpy(w.x.view(np.int16)).to(dev).view(torch.bfloat16)
+    v = None if w.v is None else torch.from_numpy(w.v).to(dev)
+    wt = None if w.w_t is None else torch.from_numpy(w.w_t).to(dev)
+    codes = torch.empty((T, n), dtype=torch.uint8, device=dev)
+    sc = torch.empty((T, n // b), dtype=torch.float16, device=dev)
+    zc = torch.empty((T, n // b), dtype=torch.float16, device=dev)
+    deq = torch.empty((T, n), dtype=torch.float32, device=dev)
+    lib = _lib.load()
+    ws_bytes = lib.narhip_rotate_dynamic_asym_int4_workspace(T, n, m, q, k, nb, b, 0)
+    assert ws_bytes == 0, "the fused hook shapes run in one kernel"
+    p = lambda t: None if t is None else ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    cs = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+    def step():
+        _lib.check(lib.narhip_rotate_dynamic_asym_int4(p(x), T, n, n, m, q, None, k, nb, p(v), p(wt), b, p(codes),
+                                                       p(sc), p(zc), p(deq), 0, None, 0, cs))
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(args.steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize(dev)
+    ms = e0.elapsed_time(e1) / args.steps
+    # x read once, codes (one byte each), fp32 deq and fp16 scale / zero written, factors read once
+    alg = T * (2 * n + n + 4 * n + 4 * n // b) + (0 if v is None else v.numel() * 4 + wt.numel() * 4)
+    achieved = alg / (ms * 1e-3) / 1e9
+    from narhip.build import sources_sha256
+    sha = sources_sha256()
+    traffic, status = measured_traffic(args.config, sha)
+    line = {
+        "metric": "fused rotate -> dynamic_asym_int4 hook (tuple out): tokens/s, 1 MI355X",
+        "value": T / (ms * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": ms, "us_per_call": ms * 1e3, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic (seeded)",
+        "config": {"workload": desc, "tokens": T, "n": n, "group": b},
+        "roofline": {"kernel": "rotate_dynamic_asym_int4 (one kernel)", "bound": "hbm", "achieved": achieved,
+                     "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBPS, "traffic": traffic,
+                     "traffic_status": status},
+        "kernel_sources_sha256": sha,
+    }
     print(json.dumps(line), flush=True)
     return 0
 

@@ -115,13 +115,17 @@ int launch_cq(const CorrQuantArgs &a, dim3 grid, hipStream_t s)
 template <int B, int KS>
 int launch_cq_t(const CorrQuantArgs &a, dim3 grid, hipStream_t s)
 {
+    if constexpr (KS == 2) {
+        if (a.tpg == 32) return launch_cq<B, KS, 8>(a, grid, s);
+    }
     return a.tpg == 16 ? launch_cq<B, KS, 4>(a, grid, s) : launch_cq<B, KS, 1>(a, grid, s);
 }
 
 }  // namespace
 
 // A workgroup owns one 128-channel block and tpg 16-token tiles (tpg / 4 per
-// wave): 16 tiles where that still leaves about 2048 workgroups or more, else 4.
+// wave): 16 tiles where that still leaves about 2048 workgroups or more, else 4
+// (32 at k > 32 on the largest shapes).
 int launch_corr_quant(CorrQuantArgs a, int b, hipStream_t s)
 {
     if (a.T == 0) return NARHIP_OK;
@@ -131,6 +135,11 @@ int launch_corr_quant(CorrQuantArgs a, int b, hipStream_t s)
     a.ncb = a.n / CQ_CB;
     const int64_t tiles = (a.T + 15) / 16;
     a.tpg = tiles * a.ncb >= 16 * 2048 ? 16 : 4;
+    // k > 32: the W'' terms staged per workgroup are 48 KB; twice the tiles per
+    // workgroup where that still leaves 2048 workgroups or more (down_proj 70B,
+    // 16384 x 28672: 1463 -> 1413 us per call; 64 tiles, code unrolled 16 times
+    // per wave, runs twice as slow)
+    if (ks == 2 && tiles * a.ncb >= 32 * 2048) a.tpg = 32;
     const int64_t groups = (tiles + a.tpg - 1) / a.tpg;
     const int64_t blocks = 8 * a.ncb * ((groups + 7) / 8);
     if (blocks > 0x7fffffff) return fail(NARHIP_EUNSUPPORTED, "too many tokens");
