@@ -326,8 +326,20 @@ def bench_transform_f16(args, w, dev) -> int:
     v = torch.from_numpy(w.v).to(dev)
     wt = torch.from_numpy(w.w_t).to(dev)
 
+    from narhip import _lib
+    lib = _lib.load()
+    T, n, k = w.tokens, w.n, w.k
+    ws_bytes = lib.narhip_transform_f16_workspace(T, n, k)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    p = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    cs = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
     def step(i: int) -> None:
-        ops.transform_f16(xs[i % R], wt, v=v, had_q=128, out=outs[i % R])
+        if args.api == "op":
+            ops.transform_f16(xs[i % R], wt, v=v, had_q=128, out=outs[i % R])
+            return
+        _lib.check(lib.narhip_transform_f16(p(xs[i % R]), T, n, n, 128, p(v), None, 0, p(wt), k, p(outs[i % R]),
+                                            p(ws), ws_bytes, cs))
 
     for i in range(args.warmup):
         step(i)
