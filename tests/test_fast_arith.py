@@ -5,8 +5,9 @@
   (csrc/narhip_device.hpp, div_sqrt_q); for Q = 128 and 512 as
   fma(v, HI, v * LO) with 1/c split in two fp32 pieces, with the division for
   |v| < 2^-90.  tests/native/div_sqrt_check.c runs the same fp32 operations;
-  this test scans a strided subset of all 2^32 bit patterns
-  (NARHIP_FULL_DIV_SCAN=1 scans all of them).
+  this test scans every finite fp32 pattern for the widths the kernels divide
+  by (128 and 512 split, 2048 and 8192), in 8 processes, and a strided subset
+  for the other widths (NARHIP_FULL_DIV_SCAN=1 scans all of them).
 * Quantizer: rint((x - z) * RN(1/s)) with the exact division only for lanes
   within 2^-18 of a half-integer (quant_code_fast).  Checked against
   rint(RN((x - z) / s)) on random groups and on constructed near-ties.
@@ -22,7 +23,20 @@ import numpy as np
 import pytest
 
 HERE = Path(__file__).resolve().parent
-QS = (2, 8, 12, 28, 32, 128, 512, 2048)
+QS = (2, 8, 12, 28, 32, 128, 512, 2048, 8192)
+
+
+# widths the kernels divide by with the reciprocal-and-correction form: every
+# finite fp32 pattern is scanned (8 processes); the other widths on a stride
+KERNEL_QS = (2048, 8192)
+
+
+def _parallel_scan(exe: Path, args_of_phase) -> list[list[int]]:
+    procs = [subprocess.Popen([str(exe), *args_of_phase(ph)], stdout=subprocess.PIPE, text=True)
+             for ph in range(8)]
+    outs = [p.communicate()[0] for p in procs]
+    assert all(p.returncode == 0 for p in procs)
+    return [list(map(int, o.split())) for o in outs]
 
 
 @pytest.mark.skipif(shutil.which("gcc") is None, reason="gcc not available")
@@ -35,11 +49,18 @@ def test_div_sqrt_matches_ieee_division():
         stride, phase = (1, 0) if full else (4099, 17)
         out = subprocess.run([str(exe), str(stride), str(phase), *map(str, QS)], check=True,
                              capture_output=True, text=True).stdout
-    rows = [tuple(map(int, line.split())) for line in out.strip().splitlines()]
-    assert [r[0] for r in rows] == list(QS)
-    for q, bad, checked in rows:
-        assert checked > 1_000_000
-        assert bad == 0, f"Q={q}: {bad} mismatches"
+        rows = [tuple(map(int, line.split())) for line in out.strip().splitlines()]
+        assert [r[0] for r in rows] == list(QS)
+        for q, bad, checked in rows:
+            assert checked > 1_000_000
+            assert bad == 0, f"Q={q}: {bad} mismatches"
+        if not full:
+            for q in KERNEL_QS:
+                parts = _parallel_scan(exe, lambda ph: ["8", str(ph), str(q)])
+                bad = sum(p[1] for p in parts)
+                checked = sum(p[2] for p in parts)
+                assert checked > 4_000_000_000, q
+                assert bad == 0, f"Q={q}: {bad} mismatches over every finite pattern"
 
 
 def _split_constants():
@@ -69,15 +90,17 @@ def test_split_division_matches_ieee_division():
         exe = Path(tmp) / "div_sqrt_check"
         subprocess.run(["gcc", "-O2", "-ffp-contract=off", "-frounding-math", "-o", str(exe),
                         str(HERE / "native" / "div_sqrt_check.c"), "-lm"], check=True)
-        stride, phase = (1, 0) if full else (4099, 17)
-
-        def scan(q, hi, lo):
+        def scan(q, hi, lo, stride=4099, phase=17):
             out = subprocess.run([str(exe), "split", str(stride), str(phase), str(q), hi, lo],
                                  check=True, capture_output=True, text=True).stdout.split()
             return int(out[1]), int(out[2])
 
+        def scan_all(q, hi, lo):
+            parts = _parallel_scan(exe, lambda ph: ["split", "8", str(ph), str(q), hi, lo])
+            return sum(p[1] for p in parts), sum(p[2] for p in parts)
+
         for q, hi, lo in _split_constants():
-            bad, checked = scan(q, hi, lo)
+            bad, checked = (scan(q, hi, lo, 1, 0) if full else scan_all(q, hi, lo))
             assert checked > 1_000_000
             assert bad == 0, f"Q={q}: {bad} mismatches"
             # a dropped low piece (plain multiplication by RN(1/c)) is caught
