@@ -115,20 +115,39 @@ def special_case(name: str, t: int, n: int) -> torch.Tensor:
     return x.expand(t, -1).contiguous()
 
 
-@pytest.mark.parametrize("name", SPECIAL)
-def test_special_inputs(name):
-    print(f"[test_special_inputs] {name}", flush=True)
+@pytest.mark.parametrize("tokens", [1, 2048, 32768])
+@pytest.mark.parametrize("name", SPECIAL + ("repeated_rows",))
+def test_special_inputs(name, tokens):
+    """The cases of e28_v2/verify.py:40-49 at its token counts 1, 2048, 32768.
+
+    The rows of each input repeat with a period P (1 for the special rows,
+    256 seeded rows in place of the reference's repeated real activations), so
+    the full-size output is checked by periodicity on the GPU (rows are
+    transformed independently: every period must equal the first, bit for
+    bit) and the first period against the oracle.
+    """
+    print(f"[test_special_inputs] {name} tokens={tokens}", flush=True)
     n = 8192
     y, w = factors(n, seed=1)
-    x = special_case(name, 33, n)
+    if name == "repeated_rows":
+        period = min(tokens, 256)
+        first = rows(period, n, seed=17)
+    else:
+        period = 1
+        first = special_case(name, 1, n)
+    reps = tokens // period
+    xd = first.cuda().repeat(reps, 1)
     mod = nk.NARDownTransform(torch.from_numpy(y), torch.from_numpy(w), K, {}).cuda()
-    out = mod(x.cuda())
+    out = mod(xd)
     torch.cuda.synchronize()
+    assert out.shape == (tokens, n)
     assert bool(torch.isfinite(out).all())
-    ref = O.rotate(x.float().numpy(), 1, 128, v=y, wt=w)
-    worst, frac = f16_ulp_report(out, ref)
+    head = out[:period]
+    assert torch.equal(out.view(reps, period, n), head.unsqueeze(0).expand(reps, period, n))
+    ref = O.rotate(first.float().numpy(), 1, 128, v=y, wt=w)
+    worst, frac = f16_ulp_report(head, ref)
     assert worst <= 1 and frac <= 1e-4, (worst, frac)
-    e28_accept(out, x, y, w)
+    e28_accept(head, first, y, w)
     if name == "zero":
         assert not out.float().abs().max().item()
 
