@@ -488,7 +488,7 @@ def bench_w4a4(args, dev) -> int:
     line = {
         "metric": "group-asymmetric W4A4 GEMM (packed INT4 A and W, fp16 scale/zero per 128): tokens/s, 1 MI355X",
         "value": T / (ms * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-        "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+        "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp8 (e4m3 INT4 codes)",
         "data": "synthetic (seeded codes and scales)",
         "config": {"workload": f"w4a4_8b: {T} x {n} INT4 activations, {O} x {n} INT4 weights, b=128, fp32 out",
                    "tokens": T, "n": n, "out_features": O},

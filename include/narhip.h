@@ -229,7 +229,8 @@ int narhip_rank_projection_f16(const void *x_f16, int64_t tokens, int64_t n, int
  * for activations (codes uint8 [tokens, n/2], low nibble = even channel; fp16
  * scales / zeros [tokens, n/128]: the output of narhip_rotate_quant) and
  * weights in the same format [out_features, ...]; out fp32 [tokens, ld_out].
- * Per group: integer code products on int8 MFMA, then
+ * Per group: the code products sum qA qW exactly on the fp8 matrix cores
+ * (a code byte c read as e4m3 is c * 2^-9), then
  * sA sW sum qA qW + sA SA zW + zA (sW SW + 128 zW) in fp32 (SA, SW the code
  * sums).  group must be 128.  With few output tiles (decode) the groups are
  * split over workgroups and the partials summed in split order.  The reference documents this form and runs no

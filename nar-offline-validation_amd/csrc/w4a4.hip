@@ -10,27 +10,37 @@
 //
 // with SA, SW the group's code sums (the four-term form of
 // quarot-llama3/e28_v2/docs/quantizer_contract.md:134-140, the last two terms
-// regrouped per side).  The integer code products run on
-// v_mfma_i32_16x16x64_i8 (codes 0..15 as int8, two K steps per group); the two
-// rank-2 terms on v_mfma_f32_16x16x4_f32, accumulated straight into the fp32
-// output tile; the first term's scale product costs three VALU operations per
-// (token, output, group).
+// regrouped per side).
+//
+// The code products run on the fp8 matrix cores: a code byte c (0..15) read as
+// OCP e4m3 is exactly c * 2^-9 (c < 8 are the subnormals m * 2^-9, 8..15 have
+// exponent field 1 and mantissa c - 8), so one v_mfma_scale_f32_16x16x128_f8f6f4
+// on the unpacked code bytes gives sum_j qA qW * 2^-18 for a whole group,
+// exactly (integers below 2^15 times a power of two), already in fp32.  The
+// 2^18 goes into the staged weight scale, so the first term costs one multiply
+// and one FMA per (token, output, group).  The two offset terms run as a rank-4
+// product on v_mfma_f32_16x16x4_f32, two groups per instruction.
 //
 // Block: 128 tokens x 128 outputs, four waves of 64 x 64 (4 x 4 MFMA tiles).
-// Per group the block unpacks its A and W codes once into LDS as int8 (the
+// Per group the block unpacks its A and W codes once into LDS as bytes (the
 // low-nibble bytes, then the high-nibble bytes, of each packed word: the same
 // channel order on both sides, so the contraction pairs equal channels), sums
-// the codes of each row with v_dot4, and stages the per-row scalars; the next
-// group's packed codes are loaded during the current group's MFMAs (two LDS
-// buffers, one barrier per group).  Dispatch is round-robin over the 8 XCDs by
-// linear block id, so when gridDim.x (weight tiles) is a multiple of 8 all
-// blocks of one weight tile run on one XCD and share its L2.
+// the codes of each row with v_dot8 and stages the per-row scalars: the scales
+// beside the codes (two buffers, one barrier per group), the offset-term
+// scalars in a three-slot ring, so that a pair of groups can be read after the
+// first group's code buffer is reused.  Packed codes travel in two register
+// sets, loaded two groups ahead.  Within a group each code MFMA is issued
+// ahead of four VALU operations (scale terms of the tile before it, unpack of
+// the next group).  Dispatch is round-robin over the 8 XCDs by linear block
+// id, so when gridDim.x (weight tiles) is a multiple of 8 all blocks of one
+// weight tile run on one XCD and share its L2.
 #pragma once
 #include "narhip_device.hpp"
 
 namespace narhip {
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 struct W4A4Args {
@@ -47,11 +57,17 @@ struct W4A4Args {
 };
 
 constexpr int WQ_TM = 128, WQ_TN = 128;           // block tile (tokens, outputs)
-constexpr int WQ_ROWB = 144;                      // unpacked row: 128 int8 codes + 16 pad (conflict-free b128 reads)
+constexpr int WQ_ROWB = 144;                      // unpacked row: 128 code bytes + 16 pad (conflict-free b128 reads)
 constexpr int WQ_AB = WQ_TM * WQ_ROWB;            // A codes per buffer
 constexpr int WQ_WB = WQ_TN * WQ_ROWB;            // W codes per buffer
-constexpr int WQ_SB = (WQ_TM + WQ_TN) * 3 * 4;    // row scalars: A {sA, sA*SA, zA}, W {sW, zW, sW*SW + 128 zW}
-constexpr int WQ_BUF = WQ_AB + WQ_WB + WQ_SB;
+constexpr int WQ_SB = (WQ_TM + WQ_TN) * 4;        // scale scalars: A sA, W sW 2^18
+constexpr int WQ_BUF = WQ_AB + WQ_WB + WQ_SB;     // one group's codes and scales (two buffers)
+constexpr int WQ_RB = (WQ_TM + WQ_TN) * 2 * 4;    // one group's offset-term scalars (three-slot ring):
+                                                  // A {sA SA, zA}, W {zW, sW SW + 128 zW}
+constexpr int WQ_LDS = 2 * WQ_BUF + 3 * WQ_RB;
+static_assert(WQ_LDS <= 81920, "two workgroups per CU share 160 KiB of LDS");
+constexpr float WQ_E4M3_UNIT2 = 262144.0f;        // 2^18 = 1 / (2^-9 * 2^-9)
+constexpr int WQ_E8M0_ONE = 127;                  // MFMA block scale 2^0
 
 // One thread's share of a group: 32 packed bytes (64 codes) of one row.
 struct WqStage {
@@ -77,11 +93,9 @@ __device__ __forceinline__ uint32_t wq_unpack(const WqStage &st, uint8_t *dst)
     uint32_t sum = 0;
 #pragma unroll
     for (int j = 0; j < 8; j++) {
-        const uint32_t lo = w[j] & 0x0F0F0F0Fu, hi = (w[j] >> 4) & 0x0F0F0F0Fu;
-        o[2 * j] = lo;
-        o[2 * j + 1] = hi;
-        sum = __builtin_amdgcn_udot4(lo, 0x01010101u, sum, false);
-        sum = __builtin_amdgcn_udot4(hi, 0x01010101u, sum, false);
+        o[2 * j] = w[j] & 0x0F0F0F0Fu;
+        o[2 * j + 1] = (w[j] >> 4) & 0x0F0F0F0Fu;
+        sum = __builtin_amdgcn_udot8(w[j], 0x11111111u, sum, false);
     }
     uint4 *d = reinterpret_cast<uint4 *>(dst);
 #pragma unroll
@@ -89,17 +103,25 @@ __device__ __forceinline__ uint32_t wq_unpack(const WqStage &st, uint8_t *dst)
     return sum;
 }
 
+__device__ __forceinline__ i32x8 wq_frag(const uint8_t *p)
+{
+    const i32x4 lo = *reinterpret_cast<const i32x4 *>(p), hi = *reinterpret_cast<const i32x4 *>(p + 16);
+    return i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
 template <int = 0>
 __global__ void __launch_bounds__(256, 2)
 w4a4_kernel(W4A4Args a)
 {
-    __shared__ __align__(16) uint8_t lds[2 * WQ_BUF];
+    __shared__ __align__(16) uint8_t lds[WQ_LDS];
+    float *const ring = reinterpret_cast<float *>(lds + 2 * WQ_BUF);
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int wm = w & 1, wn = w >> 1;               // wave tile: tokens 64 wm.., outputs 64 wn..
     const int l16 = lane & 15, lg = lane >> 4;
     const int64_t o0 = (int64_t)blockIdx.x * WQ_TN, t0 = (int64_t)blockIdx.y * WQ_TM;
     const int G = (int)(a.n / 128);
     const int gb = (int)((int64_t)blockIdx.z * G / a.splits), ge = (int)((int64_t)(blockIdx.z + 1) * G / a.splits);
+    const int cnt = ge - gb;
     const int64_t rowbytes = a.n / 2;
 
     // loader: row lr (0..127) of both tiles, 64-code half lh of the group
@@ -110,29 +132,37 @@ w4a4_kernel(W4A4Args a)
     const uint8_t *wrow = a.wc + ow * rowbytes + lh * 32;
     const uint16_t *asr = a.as + ta * G, *azr = a.az + ta * G;
     const uint16_t *wsr = a.ws + ow * G, *wzr = a.wz + ow * G;
+    auto load = [&](WqStage &sa, WqStage &sw, int j) {
+        const int g = gb + (j < cnt ? j : cnt - 1);   // past the end: reload the last group
+        wq_load(sa, arow, asr, azr, g);
+        wq_load(sw, wrow, wsr, wzr, g);
+    };
 
-    auto stage = [&](const WqStage &sa, const WqStage &sw, uint8_t *buf) {
+    // Unpack group j into its code buffer and scalar slots; branch-free (the
+    // even thread of a row pair writes the A scalars, the odd one the W
+    // scalars) so that a group step stays one scheduling region.
+    static_assert(WQ_TM == WQ_TN, "scalar rows are addressed with one stride");
+    auto stage = [&](const WqStage &sa, const WqStage &sw, int j) {
+        uint8_t *buf = lds + (j & 1) * WQ_BUF;
         uint32_t ca = wq_unpack(sa, buf + lr * WQ_ROWB + lh * 64);
         uint32_t cw = wq_unpack(sw, buf + WQ_AB + lr * WQ_ROWB + lh * 64);
         ca += __shfl_xor(ca, 1);
         cw += __shfl_xor(cw, 1);
-        if (lh == 0) {
-            float *sc = reinterpret_cast<float *>(buf + WQ_AB + WQ_WB);
-            const float sA = f16_bits_to_f32(sa.s), zA = f16_bits_to_f32(sa.z);
-            const float sW = f16_bits_to_f32(sw.s), zW = f16_bits_to_f32(sw.z);
-            sc[lr] = sA;
-            sc[WQ_TM + lr] = sA * (float)ca;
-            sc[2 * WQ_TM + lr] = zA;
-            sc[3 * WQ_TM + lr] = sW;
-            sc[3 * WQ_TM + WQ_TN + lr] = zW;
-            sc[3 * WQ_TM + 2 * WQ_TN + lr] = __builtin_fmaf(sW, (float)cw, 128.0f * zW);
-        }
+        const bool isA = lh == 0;
+        const float sv = f16_bits_to_f32(isA ? sa.s : sw.s), zv = f16_bits_to_f32(isA ? sa.z : sw.z);
+        const float cs = (float)(isA ? ca : cw);
+        float *rs = ring + (j % 3) * (WQ_RB / 4) + lh * 2 * WQ_TM;
+        rs[lr] = isA ? sv * cs : zv;                                      // sA SA | zW
+        rs[WQ_TM + lr] = isA ? zv : __builtin_fmaf(sv, cs, 128.0f * zv);  // zA   | sW SW + 128 zW
+        reinterpret_cast<float *>(buf + WQ_AB + WQ_WB)[lh * WQ_TM + lr] = isA ? sv : sv * WQ_E4M3_UNIT2;
     };
 
-    WqStage sa, sw;
-    wq_load(sa, arow, asr, azr, gb);
-    wq_load(sw, wrow, wsr, wzr, gb);
-    stage(sa, sw, lds);
+    // two register sets of packed codes in flight: group j + 1 is loaded
+    // during group j - 1, so its latency spans two group steps
+    WqStage st[2][2];
+    load(st[0][0], st[0][1], 0);
+    load(st[1][0], st[1][1], 1);
+    stage(st[0][0], st[0][1], 0);
     __syncthreads();
 
     f32x4 acc[4][4];
@@ -141,62 +171,89 @@ w4a4_kernel(W4A4Args a)
 #pragma unroll
         for (int nt = 0; nt < 4; nt++) acc[mt][nt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    for (int g = gb; g < ge; g++) {
-        const uint8_t *buf = lds + ((g - gb) & 1) * WQ_BUF;
-        // next group's packed codes and scalars (the last group reloads itself)
-        const int gn = g + 1 < ge ? g + 1 : g;
-        wq_load(sa, arow, asr, azr, gn);
-        wq_load(sw, wrow, wsr, wzr, gn);
-
-        i32x4 d[4][4];
-#pragma unroll
-        for (int kk = 0; kk < 2; kk++) {
-            i32x4 fa[4], fb[4];
-#pragma unroll
-            for (int mt = 0; mt < 4; mt++)
-                fa[mt] = *reinterpret_cast<const i32x4 *>(buf + (wm * 64 + mt * 16 + l16) * WQ_ROWB + kk * 64 + lg * 16);
-#pragma unroll
-            for (int nt = 0; nt < 4; nt++)
-                fb[nt] = *reinterpret_cast<const i32x4 *>(buf + WQ_AB + (wn * 64 + nt * 16 + l16) * WQ_ROWB + kk * 64 +
-                                                          lg * 16);
-#pragma unroll
-            for (int mt = 0; mt < 4; mt++)
-#pragma unroll
-                for (int nt = 0; nt < 4; nt++)
-                    d[mt][nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
-                        fa[mt], fb[nt], kk ? d[mt][nt] : i32x4{0, 0, 0, 0}, 0, 0, 0);
-        }
-
-        // epilogue of the group
-        const float *sc = reinterpret_cast<const float *>(buf + WQ_AB + WQ_WB);
-        f32x4 sA4[4];
-        float pA[4], sWv[4], qB[4];
+    // rank-4 offset terms of the pair of groups (j - 1, j) (slots 0, 1 from
+    // the first, 2, 3 from the second), or of group j alone (slots 2, 3 zero)
+    auto offsets = [&](int j, bool pair) {
+        const int slot = lg < 2 ? (pair ? (j + 2) % 3 : j % 3) : j % 3;
+        const float *rs = ring + slot * (WQ_RB / 4);
+        const bool live = pair || lg < 2;
+        float pA[4], qB[4];
 #pragma unroll
         for (int mt = 0; mt < 4; mt++) {
-            const int r = wm * 64 + mt * 16;
-            sA4[mt] = *reinterpret_cast<const f32x4 *>(sc + r + 4 * lg);
-            // f32 MFMA A operand: row l16, K slot lg: (sA SA, zA, 0, 0)
-            pA[mt] = lg < 2 ? sc[(1 + lg) * WQ_TM + r + l16] : 0.0f;
+            const float v = rs[(lg & 1) * WQ_TM + wm * 64 + mt * 16 + l16];                  // (sA SA, zA)
+            pA[mt] = live ? v : 0.0f;
         }
 #pragma unroll
         for (int nt = 0; nt < 4; nt++) {
-            const int c = wn * 64 + nt * 16 + l16;
-            sWv[nt] = sc[3 * WQ_TM + c];
-            // B operand: column l16, K slot lg: (zW, sW SW + 128 zW, 0, 0)
-            qB[nt] = lg < 2 ? sc[3 * WQ_TM + (1 + lg) * WQ_TN + c] : 0.0f;
+            const float v = rs[2 * WQ_TM + (lg & 1) * WQ_TN + wn * 64 + nt * 16 + l16];   // (zW, sW SW + 128 zW)
+            qB[nt] = live ? v : 0.0f;
         }
 #pragma unroll
         for (int mt = 0; mt < 4; mt++)
 #pragma unroll
-            for (int nt = 0; nt < 4; nt++) {
+            for (int nt = 0; nt < 4; nt++)
+                acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(pA[mt], qB[nt], acc[mt][nt], 0, 0, 0);
+    };
+
+    // One group: load group j + 2 into the register set group j came in;
+    // the 16 code MFMAs with their scale terms; at the second group of a pair
+    // (PAR = 1) the pair's offset terms; unpack group j + 1; barrier.
+    auto step = [&](auto par, int j) {
+        constexpr int PAR = decltype(par)::value;
+        load(st[PAR][0], st[PAR][1], j + 2);
+        const uint8_t *buf = lds + PAR * WQ_BUF;
+        const float *sc = reinterpret_cast<const float *>(buf + WQ_AB + WQ_WB);
+        f32x4 sA4[4];
+        float sWv[4];
+#pragma unroll
+        for (int mt = 0; mt < 4; mt++) sA4[mt] = *reinterpret_cast<const f32x4 *>(sc + wm * 64 + mt * 16 + 4 * lg);
+#pragma unroll
+        for (int nt = 0; nt < 4; nt++) sWv[nt] = sc[WQ_TM + wn * 64 + nt * 16 + l16];
+
+        i32x8 fb[4];
+#pragma unroll
+        for (int nt = 0; nt < 4; nt++) fb[nt] = wq_frag(buf + WQ_AB + (wn * 64 + nt * 16 + l16) * WQ_ROWB + lg * 32);
+        f32x4 d[4][4];
+#pragma unroll
+        for (int mt = 0; mt < 4; mt++) {
+            const i32x8 fa = wq_frag(buf + (wm * 64 + mt * 16 + l16) * WQ_ROWB + lg * 32);
+#pragma unroll
+            for (int nt = 0; nt < 4; nt++)
+                d[mt][nt] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                    fa, fb[nt], f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0, WQ_E8M0_ONE, 0, WQ_E8M0_ONE);
+        }
+#pragma unroll
+        for (int mt = 0; mt < 4; mt++)
+#pragma unroll
+            for (int nt = 0; nt < 4; nt++)
 #pragma unroll
                 for (int i = 0; i < 4; i++)
-                    acc[mt][nt][i] = __builtin_fmaf(sA4[mt][i] * sWv[nt], (float)d[mt][nt][i], acc[mt][nt][i]);
-                acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(pA[mt], qB[nt], acc[mt][nt], 0, 0, 0);
-            }
-
-        stage(sa, sw, lds + ((g + 1 - gb) & 1) * WQ_BUF);
+                    acc[mt][nt][i] = __builtin_fmaf(sA4[mt][i] * sWv[nt], d[mt][nt][i], acc[mt][nt][i]);
+        if constexpr (PAR == 1) offsets(j, true);
+        // unconditional: after the last group this rewrites the other buffer
+        // and a free ring slot with a reloaded group that nothing reads
+        stage(st[1 - PAR][0], st[1 - PAR][1], j + 1);
+        // issue order: each code MFMA followed by 4 VALU operations (the
+        // scale terms of the tile before it, the unpack), so that the matrix
+        // cores and the VALU of the wave work at the same time
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+#pragma unroll
+        for (int i = 0; i < 15; i++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
         __syncthreads();
+    };
+
+    int j = 0;
+    for (; j + 1 < cnt; j += 2) {
+        step(std::integral_constant<int, 0>{}, j);
+        step(std::integral_constant<int, 1>{}, j + 1);
+    }
+    if (j < cnt) {
+        step(std::integral_constant<int, 0>{}, j);
+        offsets(j, false);      // an unpaired last group
     }
 
     // one split: the output; several: partial [blockIdx.z][T][O], summed in split order by w4a4_reduce
