@@ -52,8 +52,14 @@ rq_seg_kernel(SegArgs a)
     const int64_t seg = (int64_t)blockIdx.x * 16 + row;
     const bool active = seg < a.T * segs_per_token;
     const int64_t sg = active ? seg : 0;
-    const int64_t t = sg / segs_per_token;
-    const int64_t base = (sg % segs_per_token) * Q;   // channel offset in the token
+    // per-head rank without a scatter: segments ordered token-fastest, so the
+    // rows of a wave share one head and its V and W rows (one set of
+    // addresses per wave instead of four); otherwise token-major (a scatter
+    // then writes whole output rows per workgroup)
+    constexpr bool HEAD = MODE == RANK_LOCAL && NH == 1;
+    const bool tfast = HEAD && !a.dest;
+    const int64_t t = tfast ? sg % a.T : sg / segs_per_token;
+    const int64_t base = (tfast ? sg / a.T : sg % segs_per_token) * Q;   // channel offset in the token
     const int chunk = lane_chunk(l16);
 
     // ---- load: NH x 16-byte bf16 loads per lane
@@ -80,7 +86,6 @@ rq_seg_kernel(SegArgs a)
     // lane's 8 channels, the W rows over them and the destination row are
     // requested together with x, so the row waits on memory once (the decode
     // and KV-cache shapes are latency-bound)
-    constexpr bool HEAD = MODE == RANK_LOCAL && NH == 1;
     float vh[HEAD ? 8 * KMAX : 1], wh[HEAD ? 8 * KMAX : 1];
     if constexpr (HEAD) {
         const int64_t c0 = base + chunk * 8;
