@@ -202,8 +202,17 @@ fold_u_kernel(const float *partial, int splits, int k, int kp, int64_t T, __bf16
     const int r = (int)(idx % kp);
     double sum = 0.0;
     if (r < k) {
+        // eight partials in flight, added in split order
         const float *pp = partial + t * (int64_t)splits * k + r;
-        for (int s = 0; s < splits; s++) sum += (double)pp[(int64_t)s * k];
+        int sp = 0;
+        for (; sp + 8 <= splits; sp += 8) {
+            float f[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) f[j] = pp[(int64_t)(sp + j) * k];
+#pragma unroll
+            for (int j = 0; j < 8; j++) sum += (double)f[j];
+        }
+        for (; sp < splits; sp++) sum += (double)pp[(int64_t)sp * k];
     }
     __bf16 h, m, l;
     split3((float)sum, h, m, l);
