@@ -134,10 +134,12 @@ __device__ __forceinline__ uint32_t pack8(const float (&c)[8])
 // the dispatcher places workgroup b on XCD b % 8, so all channel blocks of a
 // token group share one XCD (its L2 merges their 2-byte scale and zero stores
 // and holds the group's u terms).
-// Three waves per SIMD at k <= 32 (168 VGPRs: two tiles of P and u, the x'
-// tile, the slow path), two at k <= 64.  TPW tiles per wave, unrolled: the whole walk is straight-line code,
-// so the compiler's wait counts are exact and the wait for tile j never waits
-// for the request of tile j + 1.
+// TPW tiles per wave, unrolled: the whole walk is straight-line code, so the
+// compiler's wait counts are exact and the wait for tile j never waits for the
+// request of tile j + 1.  Register use (gfx950 build): TPW = 1 118-128 VGPRs
+// at k <= 32 and 162-174 at k <= 64, TPW = 4 and 8 234-256 (two waves per
+// SIMD; measured faster on the large shapes than more waves with shorter
+// walks).
 template <int B, int KS, bool ROT, int TPW>
 __global__ void __launch_bounds__(256, 2)
 corr_quant_kernel(CorrQuantArgs a)
