@@ -59,6 +59,29 @@ def test_random_operands(t, o, n):
     check(run(*ops_), *ops_, n)
 
 
+@pytest.mark.parametrize("t,o,n", [(130, 256, 14336), (3, 384, 4096), (64, 128, 128)])
+def test_code_products_exact(t, o, n):
+    """Unit scales and zero offsets: every output is the integer sum of code
+    products, exact in fp32 (below 2^24), so the kernel must return it bit for
+    bit -- the fp8 reading of the code bytes (0..7 are e4m3 subnormals) and the
+    2^18 rescaling lose nothing, with or without the reduction split over
+    workgroups (t = 3: decode-sized, split partials)."""
+    print(f"[test_code_products_exact] t={t} o={o} n={n}", flush=True)
+    rng = np.random.default_rng(t + o + n)
+    a = rng.integers(0, 256, (t, n // 2), dtype=np.uint8)
+    w = rng.integers(0, 256, (o, n // 2), dtype=np.uint8)
+    a[0] = 0x11                                  # all codes 1 (the smallest subnormal) in one row
+    w[0] = 0x77                                  # all codes 7 (the largest subnormal)
+    ones = lambda r: np.full((r, n // 128), np.float16(1.0)).view(np.uint16)  # noqa: E731
+    zero = lambda r: np.zeros((r, n // 128), np.uint16)  # noqa: E731
+    y = run(a, ones(t), zero(t), w, ones(o), zero(o))
+    qa = O.unpack(a, n).astype(np.int64)
+    qw = O.unpack(w, n).astype(np.int64)
+    want = qa @ qw.T
+    assert want.max() < 2 ** 24
+    assert np.array_equal(y, want.astype(np.float32)), np.abs(y - want).max()
+
+
 def test_extreme_codes_and_zero_scales():
     print("[test_extreme_codes_and_zero_scales]", flush=True)
     rng = np.random.default_rng(3)
