@@ -49,7 +49,7 @@ rq_seg_kernel(SegArgs a)
     const int l16 = lane & 15;
     const int row = threadIdx.x >> 4;    // 16 rows per block
     const int64_t segs_per_token = a.n / Q;
-    const int64_t seg = (int64_t)blockIdx.x * 16 + row;
+    const int64_t seg = (int64_t)blockIdx.x * (blockDim.x >> 4) + row;   // 16 lanes per segment
     const bool active = seg < a.T * segs_per_token;
     const int64_t sg = active ? seg : 0;
     // per-head rank without a scatter: segments ordered token-fastest, so the
