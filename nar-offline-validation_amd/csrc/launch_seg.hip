@@ -13,18 +13,24 @@ int launch_seg_qb(const SegArgs &a, int mode, hipStream_t s)
     const int64_t segs = a.T * (a.n / Q);
     dim3 grid((unsigned)((segs + 15) / 16));
     if (grid.x == 0) return NARHIP_OK;
-    // per-head rank at Q = 128 with few segments (decode): one wave per
-    // workgroup, so the segments spread over four times as many CUs (decode
-    // V-cache 64 x 8 heads: 5.0 -> 4.5 us per kernel; at 2048 x 8 heads no gain)
-    const bool wave_groups = Q == 128 && segs <= 4096;
-    const dim3 grid64((unsigned)((segs + 3) / 4));
+    if (mode == RANK_LOCAL && Q == 128) {
+        // per-head form: grid (token tiles, heads); with few segments (decode)
+        // one wave per workgroup, so they spread over four times as many CUs
+        // (decode V-cache 64 x 8 heads: 5.0 -> 4.1 us per kernel)
+        const int64_t heads = a.n / 128;
+        if (heads > 65535) return fail(NARHIP_EUNSUPPORTED, "too many 128-channel blocks per token");
+        const int rows = segs <= 4096 ? 4 : 16;
+        const dim3 g2((unsigned)((a.T + rows - 1) / rows), (unsigned)heads), blk((unsigned)(16 * rows));
+        if (a.k <= 2) hipLaunchKernelGGL((rq_seg_kernel<Q, B, RANK_LOCAL, 2>), g2, blk, 0, s, a);
+        else if (a.k <= 4) hipLaunchKernelGGL((rq_seg_kernel<Q, B, RANK_LOCAL, 4>), g2, blk, 0, s, a);
+        else hipLaunchKernelGGL((rq_seg_kernel<Q, B, RANK_LOCAL, 8>), g2, blk, 0, s, a);
+        return check_launch("rq_seg_kernel");
+    }
     switch (mode) {
     case RANK_NONE: hipLaunchKernelGGL((rq_seg_kernel<Q, B, RANK_NONE, 0>), grid, dim3(256), 0, s, a); break;
     case RANK_LOCAL:
-        // per-block rank, compiled for the rank (KV heads: k = 2 or 4)
-        if (wave_groups && a.k <= 2) hipLaunchKernelGGL((rq_seg_kernel<Q, B, RANK_LOCAL, 2>), grid64, dim3(64), 0, s, a);
-        else if (wave_groups && a.k <= 4) hipLaunchKernelGGL((rq_seg_kernel<Q, B, RANK_LOCAL, 4>), grid64, dim3(64), 0, s, a);
-        else if (a.k <= 2) hipLaunchKernelGGL((rq_seg_kernel<Q, B, RANK_LOCAL, 2>), grid, dim3(256), 0, s, a);
+        // per-block rank at Q > 128, compiled for the rank
+        if (a.k <= 2) hipLaunchKernelGGL((rq_seg_kernel<Q, B, RANK_LOCAL, 2>), grid, dim3(256), 0, s, a);
         else if (a.k <= 4) hipLaunchKernelGGL((rq_seg_kernel<Q, B, RANK_LOCAL, 4>), grid, dim3(256), 0, s, a);
         else hipLaunchKernelGGL((rq_seg_kernel<Q, B, RANK_LOCAL, 8>), grid, dim3(256), 0, s, a);
         break;

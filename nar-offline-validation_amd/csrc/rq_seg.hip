@@ -47,19 +47,28 @@ rq_seg_kernel(SegArgs a)
     constexpr int G8 = B / 8;            // lanes per quant group (4, 8, 16)
     const int lane = threadIdx.x & 63;
     const int l16 = lane & 15;
-    const int row = threadIdx.x >> 4;    // 16 rows per block
-    const int64_t segs_per_token = a.n / Q;
-    const int64_t seg = (int64_t)blockIdx.x * (blockDim.x >> 4) + row;   // 16 lanes per segment
-    const bool active = seg < a.T * segs_per_token;
-    const int64_t sg = active ? seg : 0;
-    // per-head rank without a scatter: segments ordered token-fastest, so the
-    // rows of a wave share one head and its V and W rows (one set of
-    // addresses per wave instead of four); otherwise token-major (a scatter
-    // then writes whole output rows per workgroup)
+    const int row = threadIdx.x >> 4;    // one 16-lane row per segment
+    const int rows = blockDim.x >> 4;
+    // per-head rank: grid (token tiles, heads), so the rows of a wave are
+    // consecutive tokens of one head and share its V and W rows (one set of
+    // addresses per wave), and no 64-bit division is needed to place a row;
+    // otherwise a 1-D grid over the token-major segments
     constexpr bool HEAD = MODE == RANK_LOCAL && NH == 1;
-    const bool tfast = HEAD && !a.dest;
-    const int64_t t = tfast ? sg % a.T : sg / segs_per_token;
-    const int64_t base = (tfast ? sg / a.T : sg % segs_per_token) * Q;   // channel offset in the token
+    int64_t t, base;                     // token; channel offset in the token
+    bool active;
+    if constexpr (HEAD) {
+        const int64_t tr = (int64_t)blockIdx.x * rows + row;
+        active = tr < a.T;
+        t = active ? tr : 0;
+        base = (int64_t)blockIdx.y * Q;
+    } else {
+        const int64_t segs_per_token = a.n / Q;
+        const int64_t seg = (int64_t)blockIdx.x * rows + row;
+        active = seg < a.T * segs_per_token;
+        const int64_t sg = active ? seg : 0;
+        t = sg / segs_per_token;
+        base = (sg % segs_per_token) * Q;
+    }
     const int chunk = lane_chunk(l16);
 
     // ---- load: NH x 16-byte bf16 loads per lane
