@@ -119,14 +119,17 @@ inline size_t corr_scratch_bytes(int64_t T, int64_t n, int k)
 // partials) + xform128, which folds the chunk sums itself.
 inline bool xf_fast(int32_t had_q, int32_t k) { return had_q == 128 && k >= 1 && k <= XF_K; }
 
-// Channel chunks per projection block: the smallest divisor S of n/128 that
-// gives >= 512 blocks of 64 tokens (all of them when none does; measured:
-// 512 rather than 1024 saves 5 us at 2048 x 14336).
+// Channel chunks per projection block (proj_tok, blocks of 64 PT_TL tokens):
+// the smallest divisor S of n/128 that gives >= 256 blocks with chunks of at
+// most 8192 channels (all 128-channel blocks when none does).  Measured at
+// 2048 x 14336: 256 blocks (S = 16) 73.7 us per call against 77.4 us for 448
+// and 82-84 us for 896; at 32768 x 14336 two chunks (512 blocks) 790 us
+// against 806 us for one.
 inline int xf_splits(int64_t T, int64_t n)
 {
-    const int64_t nb = n / 128, tiles = (T + 63) / 64;
+    const int64_t nb = n / 128, tiles = (T + 64 * PT_TL - 1) / (64 * PT_TL);
     for (int64_t d = 1; d <= nb; d++)
-        if (nb % d == 0 && tiles * d >= 512) return (int)d;
+        if (nb % d == 0 && tiles * d >= 256 && n / d <= 8192) return (int)d;
     return (int)nb;
 }
 inline size_t xf_pd_bytes(int64_t T, int S) { return align256(sizeof(double) * XF_K * (size_t)T * (size_t)S); }

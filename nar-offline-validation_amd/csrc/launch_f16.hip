@@ -8,9 +8,9 @@ int launch_proj_tok(const uint16_t *x, int64_t T, int64_t n, int64_t ldx, const 
                     double *pd, float *pf, hipStream_t s, bool f16)
 {
     ProjTokArgs a{x, ldx, T, n, v, pd, pf, k, S, k % 4 == 0 && aligned16(v)};
-    const dim3 grid((unsigned)((T + 63) / 64), (unsigned)S);
-    if (f16) hipLaunchKernelGGL(proj_tok_kernel<true>, grid, dim3(256), 0, s, a);
-    else hipLaunchKernelGGL(proj_tok_kernel<false>, grid, dim3(256), 0, s, a);
+    const dim3 grid((unsigned)((T + 64 * PT_TL - 1) / (64 * PT_TL)), (unsigned)S);
+    if (f16) hipLaunchKernelGGL((proj_tok_kernel<true, PT_TL>), grid, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((proj_tok_kernel<false, PT_TL>), grid, dim3(256), 0, s, a);
     return check_launch("proj_tok_kernel");
 }
 

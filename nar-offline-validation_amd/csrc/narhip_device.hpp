@@ -227,7 +227,7 @@ __device__ __forceinline__ void fmac_dpp8(float *p, float m)
 template <int NV>
 __device__ __forceinline__ void fwht_xlane_signed(float (&v)[NV], const float (&sj)[4])
 {
-    static_assert(NV % 8 == 0 && NV >= 16, "blocks of 8, two or more per stage");
+    static_assert(NV % 8 == 0, "blocks of 8");
 #pragma unroll
     for (int b = 0; b < NV; b += 8) fmac_dpp8<0>(v + b, sj[0]);
 #pragma unroll
@@ -529,6 +529,36 @@ __device__ __forceinline__ void div_sqrt_q_fast(float (&v)[NV], float c, float r
             const float r = __builtin_fmaf(q0, c, -v[i]);
             v[i] = __builtin_fmaf(-r, rc, q0);
         }
+    }
+}
+
+// FWHT_128 of a 16-lane row (8 values per lane) and RN(v / fp32(sqrt 128)),
+// bit-identical to fwht_row<1> followed by div_sqrt_q<128>: the cross-lane
+// stages in the signed form (one v_fmac_f32_dpp per value instead of a DPP move
+// and an fma) with sigma folded into the split-constant division.  A wave in
+// which any result is below div_sqrt_q_min (zeros, whose sign can differ in
+// the signed form) or NaN redoes its rows from the input with the plain stages
+// and the checked division.
+__device__ __forceinline__ void fwht128_div(float (&v)[8], int chunk, float sq, float rsq)
+{
+    float in[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) in[i] = v[i];
+    const float sj[4] = {(chunk & 1) ? -1.0f : 1.0f, (chunk & 2) ? -1.0f : 1.0f, (chunk & 4) ? -1.0f : 1.0f,
+                         (chunk & 8) ? -1.0f : 1.0f};
+    fwht_lane_stages<1>(v);
+    fwht_xlane_signed(v, sj);
+    bool odd = false;
+#pragma unroll
+    for (int i = 0; i < 8; i++) odd |= !(__builtin_fabsf(v[i]) >= div_sqrt_q_min<128>());
+    if (__builtin_expect(__any(odd), 0)) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = in[i];
+        fwht_row<1>(v, chunk);
+        div_sqrt_q<128>(v, sq, rsq);
+    } else {
+        const float sigma = sj[0] * sj[1] * sj[2] * sj[3];
+        div_sqrt_q_fast<128>(v, sigma * sq, sigma * rsq);
     }
 }
 

@@ -172,10 +172,13 @@ rq_seg_kernel(SegArgs a)
             for (int e = 0; e < 8; e++) v[h * 8 + e] *= a.signs[base + h * 128 + chunk * 8 + e];
     }
 
-    // ---- FWHT_Q
-    fwht_row<NH>(v, chunk);
-    // normalisation: fp32 division by fp32(sqrt(Q))
-    div_sqrt_q<Q>(v, a.sq, a.rsq);
+    // ---- FWHT_Q, then the normalisation: fp32 division by fp32(sqrt(Q))
+    if constexpr (NH == 1) {
+        fwht128_div(v, chunk, a.sq, a.rsq);
+    } else {
+        fwht_row<NH>(v, chunk);
+        div_sqrt_q<Q>(v, a.sq, a.rsq);
+    }
 
     // ---- rank-k correction: x' = Hx - RN32(sum_r u_r W[r, i])
     if constexpr (HEAD) {

@@ -9,22 +9,24 @@
 // Two streaming passes over x, each organised so that the factor it needs
 // stays on chip for many tokens instead of being re-read per token:
 //
-//   proj_tok_kernel   one lane per token (64 tokens per block), the block's
-//                     channel chunk streamed through LDS in 128-channel tiles
-//                     of x and of V (converted to fp64 as it is staged;
+//   proj_tok_kernel   two tokens per lane (128 tokens per block), the
+//                     block's channel chunk streamed through LDS in 64-channel
+//                     tiles of x and of V (converted to fp64 as it is staged;
 //                     double-buffered, one barrier per tile); each V row is
-//                     read by a whole wave at one address (LDS broadcast).
-//                     fp64 FMAs; fp64 sums per channel chunk, or, with one
-//                     chunk, u = RN32(sum) itself.
+//                     read by a whole wave at one address (LDS broadcast) and
+//                     used for both tokens of every lane.  fp64 FMAs; fp64
+//                     sums per channel chunk, or, with one chunk, u = RN32(sum)
+//                     itself.
 //   xform128_kernel   one 16-lane row per 128-channel segment, 16 segments per
 //                     block; each lane keeps W^T for its 8 channels in
 //                     registers as fp64 and loops over a range of tokens (x
 //                     prefetched XF_PF tokens ahead).  u comes by scalar loads:
 //                     as stored, or RN32 of the chunk sums (or of the caller's
 //                     fp32 partials) added in chunk order.  The
-//                     butterflies, the division and the fp64 correction sum are
-//                     those of the segment kernel, so the fp32 values equal its;
-//                     then fp16 out, or (QUANT) the group-128 INT4 quantizer.
+//                     butterflies (fwht128_div), the division and the fp64
+//                     correction sum are those of the segment kernel, so the
+//                     fp32 values equal its; then fp16 out, or (QUANT) the
+//                     group-128 INT4 quantizer.
 #pragma once
 #include "narhip_device.hpp"
 
@@ -42,91 +44,122 @@ struct ProjTokArgs {
     bool v4;                  // k % 4 == 0 and v 16-byte aligned: V rows by float4 loads
 };
 
-constexpr int PT_TC = 128;                  // channels per LDS tile
-constexpr int PT_ROWB = PT_TC * 2 + 16;     // padded x row (272 B: conflict-free b128 column reads)
-constexpr int PT_XB = 64 * PT_ROWB;         // x tile bytes
-constexpr int PT_VB = PT_TC * XF_K * 8;     // V tile bytes (fp64)
-constexpr int PT_BUF = PT_XB + PT_VB;
+// proj_tok tiles: TL tokens per lane (64 TL tokens per block), TC channels per
+// LDS tile, TC / 4 per wave.  Each V row read from LDS (one broadcast address
+// per wave) feeds 8 TL fp64 FMAs.  The launcher uses TL = PT_TL = 2 (the LDS
+// return of the broadcast V rows bounded TL = 1: E17 8B k = 8, 2048 tokens,
+// 79.3 -> 73.7 us per call; E28 8B, 32768 tokens, 855 -> 790 us).
+constexpr int PT_TL = 2;
+template <int TL> struct PtShape {
+    static constexpr int TC = TL == 1 ? 128 : 64;      // channels per tile
+    static constexpr int ROWB = TC * 2 + 16;           // padded x row: conflict-free b128 column reads
+    static constexpr int XB = 64 * TL * ROWB;          // x tile bytes
+    static constexpr int VB = TC * XF_K * 8;           // V tile bytes (fp64)
+    static constexpr int BUF = XB + VB;
+    static constexpr int PR = TC / 8;                  // 16-byte pieces per x row
+    static constexpr int XPT = 64 * TL * PR / 256;     // x pieces per thread per tile
+    static constexpr int VPT = TC * XF_K / 256;        // V elements per thread per tile
+    static constexpr int CW = TC / 4;                  // channels per wave per tile
+    static_assert(XPT == 4 && VPT * 256 == TC * XF_K && (VPT == 2 || VPT == 4), "tile split");
+    static_assert(2 * BUF >= 4 * 64 * TL * XF_K * 8, "the cross-wave sums reuse the tile buffers");
+};
 
-template <bool F16>
+template <bool F16, int TL>
 __global__ void __launch_bounds__(256, 3)
 proj_tok_kernel(ProjTokArgs a)
 {
-    __shared__ __align__(16) uint8_t lds[2 * PT_BUF];
+    using S = PtShape<TL>;
+    __shared__ __align__(16) uint8_t lds[2 * S::BUF];
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = tid >> 6;
-    const int64_t t0 = (int64_t)blockIdx.x * 64;
+    const int64_t t0 = (int64_t)blockIdx.x * 64 * TL;
     const int64_t chunk = a.n / a.S;
     const int64_t c0 = (int64_t)blockIdx.y * chunk;
-    const int ntiles = (int)(chunk / PT_TC);
+    const int ntiles = (int)(chunk / S::TC);
 
-    // loader: x -- thread -> token row lr, 64-byte quarter lq of the tile's 256 bytes;
-    //         V -- thread -> tile elements 4 tid .. 4 tid + 3 of [128 channels][XF_K ranks]
+    // loader: x -- piece i of the thread is linear piece i * 256 + tid of the
+    //         tile (PR 16-byte pieces per row): every load instruction covers
+    //         whole rows of the tile;
+    //         V -- thread -> tile elements VPT tid .. of [TC channels][XF_K ranks]
     //         (rank slots >= k are 0), stored as fp64
-    const int lr = tid >> 2, lq = tid & 3;
-    const int64_t trow = t0 + lr < a.T ? t0 + lr : a.T - 1;
-    const uint4 *xsrc = reinterpret_cast<const uint4 *>(a.x + trow * a.ldx + c0 + lq * 32);
-    const int vc = (4 * tid) / XF_K, vr = (4 * tid) % XF_K;    // channel in the tile, first rank slot
+    // (piece i of the thread is row tid / PR + i * 256 / PR, the same column)
+    const int xr0 = tid / S::PR, xpc = tid % S::PR;
+    constexpr int XRS = 256 / S::PR;               // rows between the thread's pieces
+    auto xrow = [&](int i) __attribute__((always_inline)) {
+        const int64_t r = t0 + xr0 + i * XRS;
+        return reinterpret_cast<const uint4 *>(a.x + (r < a.T ? r : a.T - 1) * a.ldx + c0) + xpc;
+    };
+    const uint4 *xs0 = xrow(0), *xs1 = xrow(1), *xs2 = xrow(2), *xs3 = xrow(3);
+    const int xoff = xr0 * S::ROWB + xpc * 16;
+    const int vc = (S::VPT * tid) / XF_K, vr = (S::VPT * tid) % XF_K;    // channel in the tile, first rank slot
     const float *vsrc = a.v + (c0 + vc) * a.k;
-    const int xoff = lr * PT_ROWB + lq * 64, voff = PT_XB + 32 * tid;
-    float vf[4];
+    const int voff = S::XB + 8 * S::VPT * tid;
+    float vf[S::VPT];
+    uint4 x0, x1, x2, x3;
     // branch-free: out-of-rank slots load a valid element and are replaced by 0
-    auto load_v = [&](int tile) {
-        const float *vt = vsrc + (int64_t)tile * PT_TC * a.k;
-        if (a.v4) {
-            const float4 f = *reinterpret_cast<const float4 *>(vt + (vr < a.k ? vr : 0));
-            const bool ok = vr < a.k;
-            vf[0] = ok ? f.x : 0.0f; vf[1] = ok ? f.y : 0.0f; vf[2] = ok ? f.z : 0.0f; vf[3] = ok ? f.w : 0.0f;
-        } else {
+    auto load_tile = [&](int tile) __attribute__((always_inline)) {
+        const int xo = tile * (S::TC / 8);
+        x0 = xs0[xo]; x1 = xs1[xo]; x2 = xs2[xo]; x3 = xs3[xo];
+        const float *vt = vsrc + (int64_t)tile * S::TC * a.k;
+        bool done = false;
+        if constexpr (S::VPT == 4) {
+            if (a.v4) {
+                const float4 f = *reinterpret_cast<const float4 *>(vt + (vr < a.k ? vr : 0));
+                const bool ok = vr < a.k;
+                vf[0] = ok ? f.x : 0.0f; vf[1] = ok ? f.y : 0.0f; vf[2] = ok ? f.z : 0.0f; vf[3] = ok ? f.w : 0.0f;
+                done = true;
+            }
+        }
+        if (!done) {
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
+            for (int j = 0; j < S::VPT; j++) {
                 const float f = vt[vr + j < a.k ? vr + j : 0];
                 vf[j] = vr + j < a.k ? f : 0.0f;
             }
         }
     };
-    auto store_v = [&](uint8_t *buf) {
+    auto store_tile = [&](uint8_t *buf) __attribute__((always_inline)) {
+        *reinterpret_cast<uint4 *>(buf + xoff) = x0;
+        *reinterpret_cast<uint4 *>(buf + xoff + XRS * S::ROWB) = x1;
+        *reinterpret_cast<uint4 *>(buf + xoff + 2 * XRS * S::ROWB) = x2;
+        *reinterpret_cast<uint4 *>(buf + xoff + 3 * XRS * S::ROWB) = x3;
         double2 *dv = reinterpret_cast<double2 *>(buf + voff);
-        dv[0] = make_double2((double)vf[0], (double)vf[1]);
-        dv[1] = make_double2((double)vf[2], (double)vf[3]);
+#pragma unroll
+        for (int j = 0; j < S::VPT / 2; j++) dv[j] = make_double2((double)vf[2 * j], (double)vf[2 * j + 1]);
     };
-    uint4 x0 = xsrc[0], x1 = xsrc[1], x2 = xsrc[2], x3 = xsrc[3];
-    load_v(0);
-    {
-        uint4 *d = reinterpret_cast<uint4 *>(lds + xoff);
-        d[0] = x0; d[1] = x1; d[2] = x2; d[3] = x3;
-        store_v(lds);
-    }
+    load_tile(0);
+    store_tile(lds);
     __syncthreads();
 
-    double acc[XF_K];
+    double acc[TL][XF_K];
 #pragma unroll
-    for (int r = 0; r < XF_K; r++) acc[r] = 0.0;
-    // the wave's 32 channels of each tile: x by lane = token, V rows broadcast
-    const int xme = lane * PT_ROWB + w * 64;
-    const int vme = PT_XB + w * 32 * XF_K * 8;
+    for (int i = 0; i < TL; i++)
+#pragma unroll
+        for (int r = 0; r < XF_K; r++) acc[i][r] = 0.0;
+    // the wave's CW channels of each tile: x by lane = token (TL rows), V rows broadcast
+    const int xme = lane * S::ROWB + w * S::CW * 2;
+    const int vme = S::XB + w * S::CW * XF_K * 8;
+    constexpr int WPR = S::CW / 2;                 // x words (two channels) per row
 
     for (int tile = 0; tile < ntiles; tile++) {
-        const uint8_t *buf = lds + (tile & 1) * PT_BUF;
+        const uint8_t *buf = lds + (tile & 1) * S::BUF;
         // next tile's x and V into registers (the last tile reloads itself), then
         // into the other buffer after this tile's FMAs: no branches, so the
         // loads, the FMAs and the stores stay in one schedule region
-        const int tn = tile + 1 < ntiles ? tile + 1 : tile;
-        {
-            const uint4 *xs = xsrc + tn * (PT_TC / 8);
-            x0 = xs[0]; x1 = xs[1]; x2 = xs[2]; x3 = xs[3];
-            load_v(tn);
-        }
-        const uint4 *row = reinterpret_cast<const uint4 *>(buf + xme);
-        const double2 *vt = reinterpret_cast<const double2 *>(buf + vme);
-        uint32_t wd[16];
+        load_tile(tile + 1 < ntiles ? tile + 1 : tile);
+        uint32_t wd[TL][WPR];
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const uint4 p = row[q];
-            wd[4 * q] = p.x; wd[4 * q + 1] = p.y; wd[4 * q + 2] = p.z; wd[4 * q + 3] = p.w;
+        for (int i = 0; i < TL; i++) {
+            const uint4 *row = reinterpret_cast<const uint4 *>(buf + xme + i * 64 * S::ROWB);
+#pragma unroll
+            for (int q = 0; q < WPR / 4; q++) {
+                const uint4 p = row[q];
+                wd[i][4 * q] = p.x; wd[i][4 * q + 1] = p.y; wd[i][4 * q + 2] = p.z; wd[i][4 * q + 3] = p.w;
+            }
         }
+        const double2 *vt = reinterpret_cast<const double2 *>(buf + vme);
         // V rows two channels ahead of the FMAs; the fences keep the compiler
-        // from hoisting all 128 row reads of the tile into registers
+        // from hoisting all the row reads of the tile into registers
         double2 va[XF_K / 2], vb[XF_K / 2];
 #pragma unroll
         for (int r2 = 0; r2 < XF_K / 2; r2++) {
@@ -134,54 +167,51 @@ proj_tok_kernel(ProjTokArgs a)
             vb[r2] = vt[XF_K / 2 + r2];
         }
 #pragma unroll
-        for (int c = 0; c < 32; c++) {
+        for (int c = 0; c < S::CW; c++) {
             double2 vc[XF_K / 2];
 #pragma unroll
             for (int r2 = 0; r2 < XF_K / 2; r2++) {
                 vc[r2] = va[r2];
                 va[r2] = vb[r2];
             }
-            if (c + 2 < 32) {
+            if (c + 2 < S::CW) {
 #pragma unroll
                 for (int r2 = 0; r2 < XF_K / 2; r2++) vb[r2] = vt[(c + 2) * (XF_K / 2) + r2];
             }
-            double xv;
-            if constexpr (F16) {
-                const uint32_t h = (c & 1) ? (wd[c >> 1] >> 16) : (wd[c >> 1] & 0xffffu);
-                xv = (double)f16_bits_to_f32((uint16_t)h);
-            } else {
-                xv = (double)((c & 1) ? bf16hi(wd[c >> 1]) : bf16lo(wd[c >> 1]));
-            }
 #pragma unroll
-            for (int r2 = 0; r2 < XF_K / 2; r2++) {
-                acc[2 * r2] = fma(xv, vc[r2].x, acc[2 * r2]);
-                acc[2 * r2 + 1] = fma(xv, vc[r2].y, acc[2 * r2 + 1]);
+            for (int i = 0; i < TL; i++) {
+                double xv;
+                const uint32_t h = (c & 1) ? (wd[i][c >> 1] >> 16) : (wd[i][c >> 1] & 0xffffu);
+                if constexpr (F16) xv = (double)f16_bits_to_f32((uint16_t)h);
+                else xv = (double)__uint_as_float(h << 16);
+#pragma unroll
+                for (int r2 = 0; r2 < XF_K / 2; r2++) {
+                    acc[i][2 * r2] = fma(xv, vc[r2].x, acc[i][2 * r2]);
+                    acc[i][2 * r2 + 1] = fma(xv, vc[r2].y, acc[i][2 * r2 + 1]);
+                }
             }
             __builtin_amdgcn_sched_barrier(0);
         }
-        {
-            uint8_t *nb = lds + ((tile + 1) & 1) * PT_BUF;
-            uint4 *d = reinterpret_cast<uint4 *>(nb + xoff);
-            d[0] = x0; d[1] = x1; d[2] = x2; d[3] = x3;
-            store_v(nb);
-        }
+        store_tile(lds + ((tile + 1) & 1) * S::BUF);
         __syncthreads();
     }
 
     // combine the four waves' channel quarters in wave order
-    double *red = reinterpret_cast<double *>(lds);     // [4][64][XF_K], 16 KB
+    double *red = reinterpret_cast<double *>(lds);     // [4][64 TL][XF_K]
 #pragma unroll
-    for (int r = 0; r < XF_K; r++) red[(w * 64 + lane) * XF_K + r] = acc[r];
+    for (int i = 0; i < TL; i++)
+#pragma unroll
+        for (int r = 0; r < XF_K; r++) red[(w * 64 * TL + i * 64 + lane) * XF_K + r] = acc[i][r];
     __syncthreads();
-    if (w == 0) {
-        const int64_t t = t0 + lane;
+    if (tid < 64 * TL) {
+        const int64_t t = t0 + tid;
         if (t < a.T) {
 #pragma unroll
             for (int r = 0; r < XF_K; r++) {
-                double s = red[lane * XF_K + r];
-                s += red[(64 + lane) * XF_K + r];
-                s += red[(128 + lane) * XF_K + r];
-                s += red[(192 + lane) * XF_K + r];
+                double s = red[tid * XF_K + r];
+                s += red[(64 * TL + tid) * XF_K + r];
+                s += red[(2 * 64 * TL + tid) * XF_K + r];
+                s += red[(3 * 64 * TL + tid) * XF_K + r];
                 if (a.pd) a.pd[(t * a.S + blockIdx.y) * XF_K + r] = a.S == 1 ? (double)(float)s : s;
                 else if (r < a.k) a.pf[(t * a.S + blockIdx.y) * a.k + r] = (float)s;
             }
@@ -264,8 +294,7 @@ __device__ __forceinline__ void xform_token(const XformArgs &a, const double (&W
     } else {
         f16x8_to_f32(x, v);
     }
-    fwht_row<1>(v, chunk);
-    div_sqrt_q<128>(v, a.sq, a.rsq);
+    fwht128_div(v, chunk, a.sq, a.rsq);
     double u[XF_K];
     {
         const double2 *u2 = reinterpret_cast<const double2 *>(ut);     // one LDS address per wave
