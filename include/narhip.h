@@ -50,10 +50,11 @@ int narhip_abi_version(void);
 /* Message for the last failing call on this thread ("" if none). */
 const char *narhip_last_error_string(void);
 
-/* Host memory: the +-1 Paley Hadamard factor of order m (12 or 28) that the
- * kernels use, row-major int8 [m, m].  Replaces the constructions
- * _paley_hadamard_12 (nar/extended_experiment.py:459-472) and
- * paley_hadamard_28 (nar/activation_experiments.py:114-128), unnormalised. */
+/* Host memory: the +-1 Paley Hadamard factor of order m (12, 20, 28, 68, 76
+ * or 200) that the kernels use, row-major int8 [m, m].  Replaces the
+ * constructions _paley_hadamard_12 (nar/extended_experiment.py:459-472),
+ * paley_hadamard_28 (nar/activation_experiments.py:114-128) and
+ * paley_hadamard (nar/activation_experiments.py:141-185), unnormalised. */
 int narhip_paley(int32_t m, int8_t *out_host);
 
 /* Fused rotate -> rank-k -> INT4 quantize (one call per batch of tokens).
@@ -193,10 +194,13 @@ int narhip_rotate_dynamic_asym_int4(const void *x_bf16, int64_t tokens, int64_t 
 /* The Kronecker Hadamard of each row alone, fp32 out [rows, n]:
  * (H_m (x) H_q) diag(signs) x with m in {1, 12, 20, 28} (m = 1: every aligned
  * block of q channels), q in {128, ..., 1024} (H_20: q in {128, 256}), or
- * m = 1 with q = n in {2048, 4096, 8192} (one FWHT over the row); signs fp32
- * [n] or NULL.  Replaces full_hadamard_rows (nar/activation_experiments.py:
- * 188-217) for the widths 12 * 2^j, 20 * 2^j, 28 * 2^j and 2^j <= 8192, and
- * block Hadamards. */
+ * m = 1 with q = n in {2048, 4096, 8192} (one FWHT over the row), or
+ * m in {68, 76, 200} with n = m q <= 32768, q a power of two <= 1024 (the
+ * Qwen3 widths 68 * 256, 76 * 128, 200 * 128; the fp64 product of the
+ * reference for 68 and 200); signs fp32 [n] or NULL.  Replaces
+ * full_hadamard_rows (nar/activation_experiments.py:188-217) for the widths
+ * 12 * 2^j, 20 * 2^j, 28 * 2^j, 68 * 2^j, 76 * 2^j, 200 * 2^j and
+ * 2^j <= 8192, and block Hadamards. */
 int narhip_hadamard_rows(const void *x_bf16, int64_t rows, int64_t n, int64_t ld_x, int32_t had_m, int32_t had_q,
                          const float *signs, float *out, void *stream);
 

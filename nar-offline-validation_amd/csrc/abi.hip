@@ -93,31 +93,59 @@ int gf27_sub(int a, int b)
     return r;
 }
 
+static bool small_prime(int v)
+{
+    if (v < 2) return false;
+    for (int d = 2; d * d <= v; d++)
+        if (v % d == 0) return false;
+    return true;
+}
+
+bool paley_zp(int m, int &p, int &kind)
+{
+    if (m != 12 && m != 20 && m != 68 && m != 76 && m != 200) return false;
+    if (small_prime(m - 1) && (m - 1) % 4 == 3) { p = m - 1; kind = 1; return true; }
+    if (m % 2 == 0 && small_prime(m / 2 - 1) && (m / 2 - 1) % 4 == 1) { p = m / 2 - 1; kind = 2; return true; }
+    return false;
+}
+
 int build_paley(int m, int8_t *out)
 {
     if (m == 1) { out[0] = 1; return 0; }
-    // Paley I: order p + 1 over Z_p for the primes p = 11, 19 (p = 3 mod 4),
-    // over GF(27) for 28; core entry chi(row - col), bordered by ones, minus I
-    if (m != 12 && m != 20 && m != 28) return -1;
-    const int p = m - 1;
+    // Paley I (order p + 1, p = 3 mod 4): core entry chi(row - col) over Z_p
+    // (over GF(27) for 28), bordered by ones, minus I.  Paley II (order
+    // 2(p + 1), p = 1 mod 4): the conference matrix C (core bordered by ones,
+    // zero corner) in [[C + I, C - I], [C - I, -C - I]].
+    int p = 27, kind = 1;
     const bool field = m == 28;
-    bool residue[27] = {};
+    if (!field && !paley_zp(m, p, kind)) return -1;
+    bool residue[256] = {};
     for (int v = 1; v < p; v++) residue[field ? gf27_mul(v, v) : (v * v) % p] = true;
+    auto chi = [&](int r, int c) {               // r != c, both in [1, p]
+        const int d = field ? gf27_sub(r - 1, c - 1) : ((r - c) % p + p) % p;
+        return residue[d] ? 1 : -1;
+    };
     for (int r = 0; r < m; r++)
         for (int c = 0; c < m; c++) {
-            int val = 1;
-            if (r > 0 && c > 0) {
-                int d = field ? gf27_sub(r - 1, c - 1) : ((r - c) % p + p) % p;
-                val = (d == 0 ? 0 : (residue[d] ? 1 : -1)) - (r == c ? 1 : 0);
+            int val;
+            if (kind == 1) {
+                val = (r == 0 || c == 0) ? 1 : (r == c ? -1 : chi(r, c));
+            } else {
+                const int h = p + 1;
+                const bool br = r >= h, bc = c >= h;
+                const int rr = br ? r - h : r, cc = bc ? c - h : c;
+                const int cv = rr == cc ? 0 : (rr == 0 || cc == 0) ? 1 : chi(rr, cc);
+                const int e = rr == cc ? 1 : 0;
+                val = (!br && !bc) ? cv + e : (br != bc) ? cv - e : -cv - e;
             }
             out[r * m + c] = (int8_t)val;
         }
     // H H^T = m I
     for (int r = 0; r < m; r++)
-        for (int s = 0; s < m; s++) {
+        for (int q = 0; q < m; q++) {
             int dot = 0;
-            for (int c = 0; c < m; c++) dot += out[r * m + c] * out[s * m + c];
-            if (dot != (r == s ? m : 0)) return -2;
+            for (int c = 0; c < m; c++) dot += out[r * m + c] * out[q * m + c];
+            if (dot != (r == q ? m : 0)) return -2;
         }
     return 0;
 }
@@ -612,9 +640,51 @@ static bool tuple_group_ok(int64_t n, int group)
     return group > 0 && n % group == 0 && group % 8 == 0 && group <= 512 && !(group & (group - 1));
 }
 
+// The large Paley orders of the Qwen3 widths (paley_rows.hip): no Kronecker
+// kernel, one exact kernel per row of H_m (x) H_q, fp32 out.
+static bool large_paley(int m) { return m == 68 || m == 76 || m == 200; }
+
+static int check_paley_rows(int64_t rows, int64_t n, int64_t ld_x, int32_t m, int32_t q)
+{
+    if (!pow2(q) || q > 1024 || (int64_t)m * q != n || n > PR_MAX_ELEMS)
+        return fail(NARHIP_EUNSUPPORTED, "H_%d x H_%d: need n = m q, q a power of two <= 1024, n <= %d", m, q,
+                    PR_MAX_ELEMS);
+    if (ld_x < n || ld_x % 8) return fail(NARHIP_EINVAL, "ld_x=%lld must be >= n and a multiple of 8", (long long)ld_x);
+    if (rows > 0x7fffffff) return fail(NARHIP_EUNSUPPORTED, "too many rows");
+    return NARHIP_OK;
+}
+
+static int run_paley_rows(const void *x_bf16, int64_t rows, int64_t n, int64_t ld_x, int32_t m, int32_t q,
+                          const float *signs, float *out, void *stream)
+{
+    if (int rc = check_paley_rows(rows, n, ld_x, m, q)) return rc;
+    if (rows == 0) return NARHIP_OK;
+    if (!x_bf16 || !out) return fail(NARHIP_EINVAL, "null tensor argument");
+    if (!aligned16(x_bf16) || !aligned16(out)) return fail(NARHIP_EINVAL, "x and out must be 16-byte aligned");
+    PaleyRowsArgs pa{};
+    pa.x = static_cast<const uint16_t *>(x_bf16); pa.ldx = ld_x; pa.T = rows; pa.signs = signs; pa.out = out;
+    pa.m = m; pa.q = q;
+    if (!paley_zp(m, pa.p, pa.kind)) return fail(NARHIP_EUNSUPPORTED, "no Z_p construction of order %d", m);
+    for (int v = 1; v < pa.p; v++) {
+        const int d = (v * v) % pa.p;
+        pa.residue[d >> 5] |= 1u << (d & 31);
+    }
+    // |entry|: the fp64 1/sqrt(m) for 68 and 200, whose product the reference
+    // forms in fp64; otherwise fp32(1) / fp32(sqrt m)
+    pa.fp64_product = m == 68 || m == 200;
+    pa.sq = f32_sqrt(q);
+    pa.hm = pa.fp64_product ? 1.0 / std::sqrt((double)m) : (double)(1.0f / f32_sqrt(m));
+    return launch_paley_rows(pa, static_cast<hipStream_t>(stream));
+}
+
 size_t narhip_rotate_dynamic_asym_int4_workspace(int64_t tokens, int64_t n, int32_t had_m, int32_t had_q, int32_t k,
                                                  int64_t rank_block, int32_t group, int32_t rank_mode)
 {
+    if (large_paley(had_m)) {
+        if (tokens <= 0 || !tuple_group_ok(n, group) || k != 0 || check_paley_rows(tokens, n, n, had_m, had_q))
+            return 0;
+        return align256(4 * (size_t)tokens * (size_t)n);
+    }
     Plan p;
     if (tokens < 0 || !tuple_group_ok(n, group) ||
         make_plan(tokens, n, had_m, had_q, k, rank_block, false, 0, false, rank_mode, p))
@@ -631,6 +701,26 @@ int narhip_rotate_dynamic_asym_int4(const void *x_bf16, int64_t tokens, int64_t 
                                     size_t workspace_bytes, void *stream)
 {
     clear_error();
+    if (large_paley(had_m)) {
+        // x' of the Paley rows staged in the workspace, then the hooks' quantizer
+        if (k != 0) return fail(NARHIP_EUNSUPPORTED, "H_%d rows: no rank term", had_m);
+        if (!tuple_group_ok(n, group))
+            return fail(NARHIP_EINVAL, "group size %d: need a power of two in [8, 512] dividing %lld", group,
+                        (long long)n);
+        if (tokens < 0) return fail(NARHIP_EINVAL, "bad token count %lld", (long long)tokens);
+        if (int rc = check_paley_rows(tokens, n, ld_x, had_m, had_q)) return rc;
+        if (tokens == 0) return NARHIP_OK;
+        if (!codes || !scales_f16 || !zeros_f16 || !deq) return fail(NARHIP_EINVAL, "null tensor argument");
+        if (!aligned16(deq) || (reinterpret_cast<uintptr_t>(codes) & 7u))
+            return fail(NARHIP_EINVAL, "deq must be 16-byte aligned, codes 8-byte aligned");
+        const size_t need = align256(4 * (size_t)tokens * (size_t)n);
+        if (!workspace || workspace_bytes < need)
+            return fail(NARHIP_EWORKSPACE, "workspace of %zu bytes required, %zu given", need, workspace_bytes);
+        float *rot = static_cast<float *>(workspace);
+        if (int rc = run_paley_rows(x_bf16, tokens, n, ld_x, had_m, had_q, signs, rot, stream)) return rc;
+        return launch_quant_tuple(DT_F32, rot, tokens * n, group, codes, static_cast<uint16_t *>(scales_f16),
+                                  static_cast<uint16_t *>(zeros_f16), deq, static_cast<hipStream_t>(stream));
+    }
     Plan p;
     if (int rc = make_plan(tokens, n, had_m, had_q, k, rank_block, false, 0, false, rank_mode, p)) return rc;
     if (!tuple_group_ok(n, group))
@@ -709,6 +799,7 @@ int narhip_hadamard_rows(const void *x_bf16, int64_t rows, int64_t n, int64_t ld
 {
     clear_error();
     if (rows < 0 || n <= 0) return fail(NARHIP_EINVAL, "bad shape rows=%lld n=%lld", (long long)rows, (long long)n);
+    if (large_paley(had_m)) return run_paley_rows(x_bf16, rows, n, ld_x, had_m, had_q, signs, out, stream);
     const bool full = had_m == 1 && had_q == n && fwht_rows_width(n);
     if (!full && (!pow2(had_q) || had_q < 128 || had_q > 1024))
         return fail(NARHIP_EUNSUPPORTED,

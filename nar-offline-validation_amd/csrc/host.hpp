@@ -14,6 +14,7 @@
 #include "kron_mfma.hip"
 #include "mfma.hpp"
 #include "narhip_device.hpp"
+#include "paley_rows.hip"
 #include "rank_exact.hip"
 #include "rank_mfma.hip"
 #include "rq_row.hip"
@@ -44,9 +45,12 @@ inline size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 inline int round_up(int v, int m) { return (v + m - 1) / m * m; }
 inline float f32_sqrt(int v) { return (float)std::sqrt((double)v); }
 
-// Paley I factor of order m (1, 12 or 28) as +-1 int8 [m][m]; 0 on success,
-// -1 for an unsupported order, -2 if the result fails H H^T = m I.
+// Paley factor of order m (1, 12, 20, 28, 68, 76 or 200) as +-1 int8 [m][m];
+// 0 on success, -1 for an unsupported order, -2 if the result fails H H^T = m I.
 int build_paley(int m, int8_t *out);
+// The prime and kind (1: Paley I over Z_p, 2: Paley II) of the Z_p
+// constructions (orders 12, 20, 68, 76, 200); false for the others.
+bool paley_zp(int m, int &p, int &kind);
 PaleyTable paley_table(int m);
 
 // Raise a kernel's dynamic LDS limit for blocks of 48 KB and more (the kernels
@@ -177,6 +181,8 @@ int launch_dequant(const uint8_t *codes, const uint16_t *scales, const uint16_t 
 int launch_quant_tuple(int dtype, const void *x, int64_t elems, int group, uint8_t *codes, uint16_t *scales,
                        uint16_t *zeros, void *deq, hipStream_t s);
 int launch_w4a4(const W4A4Args &a, int64_t gx, int64_t gy, float *out, hipStream_t s);
+// rows of H_m (x) H_q for the Paley orders without a Kronecker kernel (paley_rows.hip)
+int launch_paley_rows(const PaleyRowsArgs &a, hipStream_t s);
 
 }  // namespace host
 }  // namespace narhip

@@ -1,9 +1,41 @@
 // Launchers of the stand-alone kernels: dequantization, the hooks' quantizer
-// (hooks.hip) and the W4A4 GEMM (w4a4.hip).
+// (hooks.hip), the W4A4 GEMM (w4a4.hip) and the large-order Paley rows
+// (paley_rows.hip).
 #include "host.hpp"
 
 namespace narhip {
 namespace host {
+
+int launch_paley_rows(const PaleyRowsArgs &a, hipStream_t s)
+{
+    const size_t lds = sizeof(float) * (size_t)a.m * (size_t)a.q;
+    const dim3 grid((unsigned)a.T);
+    switch (a.q <= 64 ? 1 : a.q / 64) {
+    case 1:
+        if (int rc = set_lds(paley_rows_kernel<1>, lds)) return rc;
+        hipLaunchKernelGGL(paley_rows_kernel<1>, grid, dim3(PR_THREADS), lds, s, a);
+        break;
+    case 2:
+        if (int rc = set_lds(paley_rows_kernel<2>, lds)) return rc;
+        hipLaunchKernelGGL(paley_rows_kernel<2>, grid, dim3(PR_THREADS), lds, s, a);
+        break;
+    case 4:
+        if (int rc = set_lds(paley_rows_kernel<4>, lds)) return rc;
+        hipLaunchKernelGGL(paley_rows_kernel<4>, grid, dim3(PR_THREADS), lds, s, a);
+        break;
+    case 8:
+        if (int rc = set_lds(paley_rows_kernel<8>, lds)) return rc;
+        hipLaunchKernelGGL(paley_rows_kernel<8>, grid, dim3(PR_THREADS), lds, s, a);
+        break;
+    case 16:
+        if (int rc = set_lds(paley_rows_kernel<16>, lds)) return rc;
+        hipLaunchKernelGGL(paley_rows_kernel<16>, grid, dim3(PR_THREADS), lds, s, a);
+        break;
+    default:
+        return fail(NARHIP_EUNSUPPORTED, "Paley rows need q <= 1024 (q=%d)", a.q);
+    }
+    return check_launch("paley_rows_kernel");
+}
 
 int launch_dequant(const uint8_t *codes, const uint16_t *scales, const uint16_t *zeros, int64_t rows, int64_t n,
                    int group, float *out, hipStream_t s)

@@ -1,0 +1,132 @@
+// Full-row Hadamard rows for the large Paley orders of the Qwen3 widths
+// (nar/activation_experiments.py:188-217): 68 x 256 (14B), 76 x 128 (8B),
+// 200 x 128 (32B), i.e. y = (H_m (x) H_q) diag(signs) x per row, fp32 out.
+//
+// One workgroup per row.  The row goes into LDS as fp32 (times the signs),
+// every q-point segment gets the reference's FWHT stages (widths 1, 2, ..,
+// q/2, in that order) and the fp32 division by fp32(sqrt q); then each output
+// y[a][c] = RN32(sum_{a'} F[a'][c] * h[a][a']) is accumulated in fp64 over a'
+// in increasing order, with h = +-|entry|:
+//   orders 68 and 200: |entry| = fp64(1/sqrt(m)); each product is rounded in
+//     fp64 before the add (the reference forms this product in fp64);
+//   other orders: |entry| = fp32(1/sqrt(m)); the product is exact in fp64 and
+//     one fma adds it.
+// The +-1 pattern is computed per term on the scalar unit from the
+// quadratic-residue table of the construction's prime (rows by waves, so the
+// row index and the term index are wave-uniform): Paley I (order p + 1, p a
+// prime = 3 mod 4: ones bordering Q - I, Q[r][c] = chi(r - c)) or Paley II
+// (order 2(p + 1), p = 1 mod 4: [[C + I, C - I], [C - I, -C - I]] with the
+// conference matrix C bordered by ones around Q), the constructions of
+// nar/activation_experiments.py:141-185.
+//
+// Not a bandwidth kernel: m fp64 terms per output element (m = 200: 5.1 M
+// per row of 25600).  It serves the hooks' full_hadamard_rows for these widths.
+#pragma once
+#include "narhip_device.hpp"
+
+namespace narhip {
+
+constexpr int PR_MAX_ELEMS = 32768;       // m q <= 32768: the row fits 128 KB of LDS
+constexpr int PR_THREADS = 1024;
+
+struct PaleyRowsArgs {
+    const uint16_t *x;      // bf16 [T, ldx]
+    int64_t ldx, T;
+    const float *signs;     // [m q] or null
+    float *out;             // fp32 [T, m q]
+    int m, q;               // Paley order, power-of-two factor
+    int p;                  // the construction's prime
+    int kind;               // 1: Paley I, 2: Paley II
+    int fp64_product;       // 1: products rounded in fp64 (orders 68, 200)
+    float sq;               // fp32(sqrt q)
+    double hm;              // |entry| of H_m / sqrt(m) as the products use it
+    uint32_t residue[8];    // bit d set <=> d is a nonzero square mod p (p < 256)
+};
+
+// Entry (r, c) of the +-1 Paley matrix is -1 (r, c < m; wave-uniform arguments).
+__device__ __forceinline__ bool paley_neg(const PaleyRowsArgs &a, int r, int c)
+{
+    auto chi_neg = [&](int i, int j) {       // chi(i - j mod p) = -1, i != j, i, j in [1, p]
+        int d = i - j;
+        if (d < 0) d += a.p;
+        return ((a.residue[d >> 5] >> (d & 31)) & 1u) == 0;
+    };
+    if (a.kind == 1) {
+        if (r == 0 || c == 0) return false;
+        if (r == c) return true;             // Q[r][r] - 1 = -1
+        return chi_neg(r, c);
+    }
+    const int h = a.p + 1;
+    const bool br = r >= h, bc = c >= h;
+    const int rr = br ? r - h : r, cc = bc ? c - h : c;
+    int cv;                                  // conference entry C[rr][cc]
+    if (rr == cc) cv = 0;
+    else if (rr == 0 || cc == 0) cv = 1;
+    else cv = chi_neg(rr, cc) ? -1 : 1;
+    const int e = rr == cc ? 1 : 0;
+    const int v = (!br && !bc) ? cv + e : (br != bc) ? cv - e : -cv - e;
+    return v < 0;
+}
+
+// CPL output columns per lane (q = 64 CPL, or q < 64 with CPL = 1).
+template <int CPL>
+__global__ void __launch_bounds__(PR_THREADS)
+paley_rows_kernel(PaleyRowsArgs a)
+{
+    extern __shared__ __align__(16) float F[];          // [m][q]
+    const int n = a.m * a.q;
+    const int tid = threadIdx.x;
+    const uint16_t *xr = a.x + (int64_t)blockIdx.x * a.ldx;
+    for (int i = tid; i < n; i += PR_THREADS) {
+        float v = __uint_as_float((uint32_t)xr[i] << 16);
+        if (a.signs) v *= a.signs[i];
+        F[i] = v;
+    }
+    __syncthreads();
+    // FWHT_q of each segment: at width w, pair (i, i + w) in blocks of 2w
+    const int half = a.q >> 1;
+    for (int w = 1; w < a.q; w <<= 1) {
+        for (int b = tid; b < n / 2; b += PR_THREADS) {
+            const int s = b / half, j = b - s * half;
+            const int i0 = s * a.q + (j / w) * 2 * w + j % w, i1 = i0 + w;
+            const float x0 = F[i0], x1 = F[i1];
+            F[i0] = x0 + x1;
+            F[i1] = x0 - x1;
+        }
+        __syncthreads();
+    }
+    for (int i = tid; i < n; i += PR_THREADS) F[i] = F[i] / a.sq;
+    __syncthreads();
+
+    // rows of H_m by waves, columns by lanes
+    const int lane = tid & 63, wave = tid >> 6;
+    float *o = a.out + (int64_t)blockIdx.x * n;
+    for (int r = wave; r < a.m; r += PR_THREADS / 64) {
+        const int ru = __builtin_amdgcn_readfirstlane(r);
+        double acc[CPL];
+#pragma unroll
+        for (int j = 0; j < CPL; j++) acc[j] = 0.0;
+        for (int c2 = 0; c2 < a.m; c2++) {
+            const double h = paley_neg(a, ru, c2) ? -a.hm : a.hm;
+            const float *fr = F + c2 * a.q;
+#pragma unroll
+            for (int j = 0; j < CPL; j++) {
+                const int c = lane + 64 * j;
+                const double f = (double)fr[c < a.q ? c : 0];
+                if (a.fp64_product) {
+                    const double pr = f * h;
+                    acc[j] = acc[j] + pr;
+                } else {
+                    acc[j] = fma(f, h, acc[j]);
+                }
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < CPL; j++) {
+            const int c = lane + 64 * j;
+            if (c < a.q) o[ru * a.q + c] = (float)acc[j];
+        }
+    }
+}
+
+}  // namespace narhip

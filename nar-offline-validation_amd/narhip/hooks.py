@@ -12,8 +12,8 @@ HIP kernels of libnarhip.so:
       zero16 fp16 [..., G]; codes uint8 [..., G, group_size] (one per byte).
   full_hadamard_rows(x, signs) -> (H_m (x) H_q) diag(signs) x, x's shape
       nar/activation_experiments.py:188-217, for widths 28 * 2^j, 12 * 2^j,
-      20 * 2^j (j = 7, 8) and 2^j <= 8192 (the Qwen3 orders 68, 76 and 200
-      are not built and raise).  The kernels read bf16 rows: x must be bf16,
+      20 * 2^j (j = 7, 8), the Qwen3 widths 68 * 2^j, 76 * 2^j, 200 * 2^j
+      (up to 32768 channels) and 2^j <= 8192.  The kernels read bf16 rows: x must be bf16,
       or fp32 holding bf16 values (the hooks pass ``value.float()`` of a bf16
       model).
   rotate_dynamic_asym_int4(x, group_size, *, signs=None, v=None, w_t=None,

@@ -47,8 +47,9 @@ def hadamard_factors(n: int) -> tuple[int, int]:
     """(m, q) with n = m*q in the dispatch order of full_hadamard_rows
     (nar/activation_experiments.py:188-217): 28 * 2^j first, then 12 * 2^j,
     then, for widths that are not a power of two, the Qwen3 Paley orders
-    20, 68, 76 and 200 times 2^j, then a power of two.  The kernels build
-    m in {1, 12, 20, 28}; the other orders are rejected by the library."""
+    20, 68, 76 and 200 times 2^j, then a power of two.  The Kronecker
+    kernels build m in {1, 12, 20, 28}; 68, 76 and 200 run as whole rows
+    (hadamard_rows and the hooks' tuple, no rank term)."""
     def pow2(v: int) -> bool:
         return v >= 1 and not v & (v - 1)
 

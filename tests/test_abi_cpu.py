@@ -30,7 +30,7 @@ def test_library_exports_every_declared_symbol():
     assert lib.narhip_abi_version() == 1
 
 
-@pytest.mark.parametrize("m", [12, 20, 28])
+@pytest.mark.parametrize("m", [12, 20, 28, 68, 76, 200])
 def test_library_paley_equals_oracle(m):
     import narhip
     out = np.zeros((m, m), np.int8)

@@ -147,6 +147,55 @@ def test_full_hadamard_rows_paley20(n):
     assert O.rotated_error(out.cpu().numpy(), O.rotate(O.bf16_to_f32(bits), m, q)) <= 2.0 ** -21
 
 
+@pytest.mark.parametrize("n,m", [(9728, 76), (17408, 68)])
+def test_full_hadamard_rows_large_paley_golden(n, m):
+    """The Qwen3 widths 76 x 128 and 68 x 256 on the reference's own rows: the
+    oracle's arithmetic exactly, and the reference's output within the fp32
+    rounding of an m-term sum (its BLAS order is not pinned)."""
+    print(f"[test_full_hadamard_rows_large_paley_golden] n={n} m={m}", flush=True)
+    x, s, y = _golden_rows(n)
+    q = n // m
+    out = hooks.full_hadamard_rows(torch.from_numpy(x).cuda(), torch.from_numpy(s).cuda())
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    assert np.array_equal(got, O.rotate(x, m, q, signs=s))
+    f = O.rotate(x, 1, q, signs=s).reshape(-1, m, q).astype(np.float64)
+    mag = np.einsum("ab,tbc->tac", np.abs(O.paley(m).astype(np.float64)) / np.sqrt(m), np.abs(f))
+    err = np.abs(got.astype(np.float64) - y).reshape(mag.shape)
+    assert np.all(err <= m * 2.0 ** -24 * mag + 1e-30)
+
+
+@pytest.mark.parametrize("n,m,tokens", [(25600, 200, 5), (9728, 76, 33), (17408, 68, 3), (200 * 64, 200, 2)])
+def test_full_hadamard_rows_large_paley_seeded(n, m, tokens):
+    """Seeded bf16 rows (no golden rows of 200 x 128 exist), with and without
+    signs, bit-equal to the oracle; zero rows stay zero."""
+    print(f"[test_full_hadamard_rows_large_paley_seeded] n={n} m={m} tokens={tokens}", flush=True)
+    q = n // m
+    bits = _seeded_bf16(tokens, n, 3 * n + m)
+    bits[0] = 0
+    g = np.random.default_rng(n + 1)
+    s = np.where(g.random(n) < 0.5, -1.0, 1.0).astype(np.float32)
+    out = hooks.full_hadamard_rows(to_dev_bf16(bits), torch.from_numpy(s).cuda())
+    torch.cuda.synchronize()
+    ref = O.rotate(O.bf16_to_f32(bits), m, q, signs=s)
+    assert np.array_equal(out.cpu().numpy(), ref)
+    assert not out[0].any()
+    out = hooks.full_hadamard_rows(to_dev_bf16(bits[1:]), None)
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy(), O.rotate(O.bf16_to_f32(bits[1:]), m, q))
+
+
+@pytest.mark.parametrize("n,m,group", [(9728, 76, 128), (25600, 200, 64)])
+def test_fused_tuple_large_paley(n, m, group):
+    """The hooks' rotate_dynamic_asym_int4 on the Qwen3 widths: x' staged, then the quantizer, bit-exact."""
+    print(f"[test_fused_tuple_large_paley] n={n} m={m} group={group}", flush=True)
+    bits = _seeded_bf16(6, n, 5 * n + group)
+    res = hooks.rotate_dynamic_asym_int4(to_dev_bf16(bits), group)
+    torch.cuda.synchronize()
+    ref = O.quant(O.rotate(O.bf16_to_f32(bits), m, n // m), group)
+    _assert_tuple_exact(_tuple_np(res), ref, f"n={n} m={m} group={group}")
+
+
 @pytest.mark.parametrize("n,m,q", [(2560, 20, 128), (5120, 20, 256), (3072, 12, 256), (14336, 28, 512)])
 def test_fused_kronecker_tuple_contract(n, m, q):
     print(f"[test_fused_kronecker_tuple_contract] n={n}", flush=True)
@@ -201,6 +250,13 @@ def test_fused_nonfinite_rows():
     _assert_tuple_exact(_tuple_np(res), ref, "non-finite rows")
 
 
-def test_qwen3_orders_not_built_raise():
+def test_large_paley_limits_raise():
+    # rows beyond the 32768 channels one workgroup holds (200 x 256), and a
+    # rank term on the whole-row Paley path, are not built
     with pytest.raises(ValueError):
-        hooks.full_hadamard_rows(torch.zeros((2, 9728), dtype=torch.bfloat16, device="cuda"), None)
+        hooks.full_hadamard_rows(torch.zeros((2, 51200), dtype=torch.bfloat16, device="cuda"), None)
+    w_t = torch.zeros((4, 9728), dtype=torch.float32, device="cuda")
+    v = torch.zeros((9728, 4), dtype=torch.float32, device="cuda")
+    with pytest.raises(ValueError):
+        hooks.rotate_dynamic_asym_int4(torch.zeros((2, 9728), dtype=torch.bfloat16, device="cuda"), 128,
+                                       v=v, w_t=w_t)
