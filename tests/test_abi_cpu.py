@@ -173,3 +173,26 @@ def test_noalloc_host_validation():
     rc = lib.narhip_rotate_quant_noalloc(16, 4, 1000, 1000, 1, 128, None, 0, 1000, None, None, None, None, 0,
                                          128, 16, 16, 16, None, None, 0, None)
     assert rc == -1
+
+
+@pytest.mark.parametrize("rows,n,m,q,code", [
+    (0, 9728, 76, 128, 0),          # valid Qwen3 width, nothing to do
+    (0, 25600, 200, 128, 0),
+    (2, 51200, 200, 256, -2),       # more than one workgroup's 32768 channels
+    (2, 9728, 76, 100, -2),         # q not a power of two
+    (2, 9728, 68, 128, -2),         # m q != n
+    (-1, 9728, 76, 128, -1),
+])
+def test_large_paley_rows_host_validation(rows, n, m, q, code):
+    """The whole-row Paley kernel's host checks (no launch: rows == 0 or an error first)."""
+    import narhip
+    lib = narhip.load()
+    assert lib.narhip_hadamard_rows(None, rows, n, n, m, q, None, None, None) == code
+
+
+def test_large_paley_tuple_workspace_query():
+    import narhip
+    lib = narhip.load()
+    # x' staged as fp32; a rank term is not built for these orders (0 = not supported)
+    assert lib.narhip_rotate_dynamic_asym_int4_workspace(5, 9728, 76, 128, 0, 9728, 128, 0) >= 4 * 5 * 9728
+    assert lib.narhip_rotate_dynamic_asym_int4_workspace(5, 9728, 76, 128, 8, 9728, 128, 0) == 0
