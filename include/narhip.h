@@ -182,7 +182,9 @@ int narhip_dynamic_asym_int4(const void *x, int32_t dtype, int64_t rows, int64_t
  * per-block rank (rank_block = had_q, k <= 8), the full-row FWHT of
  * n in {2048, 4096, 8192}, and H_m (x) H_q without a rank term (rank_mode
  * AUTO or MFMA); otherwise x' is staged in the workspace and quantized by a
- * second kernel. */
+ * second kernel.  had_m in {68, 76, 200} (the Qwen3 widths, n = m q <= 32768)
+ * runs the whole-row Paley kernel, with no rank term or an exact full-row one
+ * (rank_block = n, k <= 64), then the quantizer. */
 size_t narhip_rotate_dynamic_asym_int4_workspace(int64_t tokens, int64_t n, int32_t had_m, int32_t had_q,
                                                  int32_t k, int64_t rank_block, int32_t group, int32_t rank_mode);
 int narhip_rotate_dynamic_asym_int4(const void *x_bf16, int64_t tokens, int64_t n, int64_t ld_x, int32_t had_m,

@@ -655,7 +655,7 @@ static int check_paley_rows(int64_t rows, int64_t n, int64_t ld_x, int32_t m, in
 }
 
 static int run_paley_rows(const void *x_bf16, int64_t rows, int64_t n, int64_t ld_x, int32_t m, int32_t q,
-                          const float *signs, float *out, void *stream)
+                          const float *signs, float *out, void *stream, const float *corr = nullptr)
 {
     if (int rc = check_paley_rows(rows, n, ld_x, m, q)) return rc;
     if (rows == 0) return NARHIP_OK;
@@ -663,7 +663,7 @@ static int run_paley_rows(const void *x_bf16, int64_t rows, int64_t n, int64_t l
     if (!aligned16(x_bf16) || !aligned16(out)) return fail(NARHIP_EINVAL, "x and out must be 16-byte aligned");
     PaleyRowsArgs pa{};
     pa.x = static_cast<const uint16_t *>(x_bf16); pa.ldx = ld_x; pa.T = rows; pa.signs = signs; pa.out = out;
-    pa.m = m; pa.q = q;
+    pa.corr = corr; pa.m = m; pa.q = q;
     if (!paley_zp(m, pa.p, pa.kind)) return fail(NARHIP_EUNSUPPORTED, "no Z_p construction of order %d", m);
     for (int v = 1; v < pa.p; v++) {
         const int d = (v * v) % pa.p;
@@ -677,13 +677,26 @@ static int run_paley_rows(const void *x_bf16, int64_t rows, int64_t n, int64_t l
     return launch_paley_rows(pa, static_cast<hipStream_t>(stream));
 }
 
+// Workspace of the large-Paley tuple path: x' fp32, and with a full-row rank
+// term (k <= 64, exact) the projection u and the correction C before it.
+static size_t paley_tuple_bytes(int64_t tokens, int64_t n, int32_t k)
+{
+    const size_t T = (size_t)tokens, N = (size_t)n;
+    return align256(4 * T * N) + (k > 0 ? align256(4 * T * (size_t)k) + align256(4 * T * N) : 0);
+}
+static bool paley_rank_ok(int64_t n, int32_t k, int64_t rank_block)
+{
+    return k == 0 || (k >= 1 && k <= 64 && rank_block == n && n % 64 == 0);
+}
+
 size_t narhip_rotate_dynamic_asym_int4_workspace(int64_t tokens, int64_t n, int32_t had_m, int32_t had_q, int32_t k,
                                                  int64_t rank_block, int32_t group, int32_t rank_mode)
 {
     if (large_paley(had_m)) {
-        if (tokens <= 0 || !tuple_group_ok(n, group) || k != 0 || check_paley_rows(tokens, n, n, had_m, had_q))
+        if (tokens <= 0 || !tuple_group_ok(n, group) || !paley_rank_ok(n, k, rank_block) ||
+            check_paley_rows(tokens, n, n, had_m, had_q))
             return 0;
-        return align256(4 * (size_t)tokens * (size_t)n);
+        return paley_tuple_bytes(tokens, n, k);
     }
     Plan p;
     if (tokens < 0 || !tuple_group_ok(n, group) ||
@@ -702,8 +715,12 @@ int narhip_rotate_dynamic_asym_int4(const void *x_bf16, int64_t tokens, int64_t 
 {
     clear_error();
     if (large_paley(had_m)) {
-        // x' of the Paley rows staged in the workspace, then the hooks' quantizer
-        if (k != 0) return fail(NARHIP_EUNSUPPORTED, "H_%d rows: no rank term", had_m);
+        // x' of the Paley rows staged in the workspace (with a full-row rank
+        // term: exact projection and correction first), then the hooks' quantizer
+        if (!paley_rank_ok(n, k, rank_block))
+            return fail(NARHIP_EUNSUPPORTED, "H_%d rows: rank term needs k <= 64 over the whole row, n %% 64 == 0",
+                        had_m);
+        if (k > 0 && (!v || !w_t)) return fail(NARHIP_EINVAL, "rank factors missing");
         if (!tuple_group_ok(n, group))
             return fail(NARHIP_EINVAL, "group size %d: need a power of two in [8, 512] dividing %lld", group,
                         (long long)n);
@@ -713,11 +730,20 @@ int narhip_rotate_dynamic_asym_int4(const void *x_bf16, int64_t tokens, int64_t 
         if (!codes || !scales_f16 || !zeros_f16 || !deq) return fail(NARHIP_EINVAL, "null tensor argument");
         if (!aligned16(deq) || (reinterpret_cast<uintptr_t>(codes) & 7u))
             return fail(NARHIP_EINVAL, "deq must be 16-byte aligned, codes 8-byte aligned");
-        const size_t need = align256(4 * (size_t)tokens * (size_t)n);
+        const size_t need = paley_tuple_bytes(tokens, n, k);
         if (!workspace || workspace_bytes < need)
             return fail(NARHIP_EWORKSPACE, "workspace of %zu bytes required, %zu given", need, workspace_bytes);
         float *rot = static_cast<float *>(workspace);
-        if (int rc = run_paley_rows(x_bf16, tokens, n, ld_x, had_m, had_q, signs, rot, stream)) return rc;
+        float *corr = nullptr;
+        if (k > 0) {
+            hipStream_t hs = static_cast<hipStream_t>(stream);
+            float *u = reinterpret_cast<float *>(static_cast<char *>(workspace) + align256(4 * (size_t)tokens * (size_t)n));
+            corr = reinterpret_cast<float *>(reinterpret_cast<char *>(u) + align256(4 * (size_t)tokens * (size_t)k));
+            if (int rc = launch_proj_exact(static_cast<const uint16_t *>(x_bf16), tokens, n, ld_x, v, k, 1, u, hs))
+                return rc;
+            if (int rc = launch_corr_exact(u, 1, k, w_t, tokens, n, corr, hs)) return rc;
+        }
+        if (int rc = run_paley_rows(x_bf16, tokens, n, ld_x, had_m, had_q, signs, rot, stream, corr)) return rc;
         return launch_quant_tuple(DT_F32, rot, tokens * n, group, codes, static_cast<uint16_t *>(scales_f16),
                                   static_cast<uint16_t *>(zeros_f16), deq, static_cast<hipStream_t>(stream));
     }

@@ -19,8 +19,11 @@
 // conference matrix C bordered by ones around Q), the constructions of
 // nar/activation_experiments.py:141-185.
 //
-// Not a bandwidth kernel: m fp64 terms per output element (m = 200: 5.1 M
-// per row of 25600).  It serves the hooks' full_hadamard_rows for these widths.
+// A full-row rank term arrives as C = RN32(u W^T) (corr_exact_kernel) and is
+// subtracted in fp32 at the store, x' = P - C as the reference's
+// reference_transform.  Not a bandwidth kernel: m fp64 terms per output
+// element (m = 200: 5.1 M per row of 25600).  It serves the hooks'
+// full_hadamard_rows and rotate-then-quantize for these widths.
 #pragma once
 #include "narhip_device.hpp"
 
@@ -34,6 +37,7 @@ struct PaleyRowsArgs {
     int64_t ldx, T;
     const float *signs;     // [m q] or null
     float *out;             // fp32 [T, m q]
+    const float *corr;      // fp32 [T, m q] rank-k term C (out = P - C), or null
     int m, q;               // Paley order, power-of-two factor
     int p;                  // the construction's prime
     int kind;               // 1: Paley I, 2: Paley II
@@ -121,10 +125,14 @@ paley_rows_kernel(PaleyRowsArgs a)
                 }
             }
         }
+        const float *cr = a.corr ? a.corr + (int64_t)blockIdx.x * n : nullptr;
 #pragma unroll
         for (int j = 0; j < CPL; j++) {
             const int c = lane + 64 * j;
-            if (c < a.q) o[ru * a.q + c] = (float)acc[j];
+            if (c < a.q) {
+                const float pv = (float)acc[j];
+                o[ru * a.q + c] = cr ? pv - cr[ru * a.q + c] : pv;
+            }
         }
     }
 }

@@ -193,6 +193,8 @@ def test_large_paley_rows_host_validation(rows, n, m, q, code):
 def test_large_paley_tuple_workspace_query():
     import narhip
     lib = narhip.load()
-    # x' staged as fp32; a rank term is not built for these orders (0 = not supported)
+    # x' staged as fp32; with a full-row rank term also u and C (0 = not supported)
     assert lib.narhip_rotate_dynamic_asym_int4_workspace(5, 9728, 76, 128, 0, 9728, 128, 0) >= 4 * 5 * 9728
-    assert lib.narhip_rotate_dynamic_asym_int4_workspace(5, 9728, 76, 128, 8, 9728, 128, 0) == 0
+    assert lib.narhip_rotate_dynamic_asym_int4_workspace(5, 9728, 76, 128, 8, 9728, 128, 0) >= 8 * 5 * 9728
+    assert lib.narhip_rotate_dynamic_asym_int4_workspace(5, 9728, 76, 128, 8, 128, 128, 0) == 0   # per block
+    assert lib.narhip_rotate_dynamic_asym_int4_workspace(5, 9728, 76, 128, 65, 9728, 128, 0) == 0

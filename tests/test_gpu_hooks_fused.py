@@ -250,13 +250,30 @@ def test_fused_nonfinite_rows():
     _assert_tuple_exact(_tuple_np(res), ref, "non-finite rows")
 
 
+@pytest.mark.parametrize("n,m,k,tokens,group", [(9728, 76, 8, 21, 128), (17408, 68, 32, 3, 64), (25600, 200, 16, 2, 128)])
+def test_fused_tuple_large_paley_rank(n, m, k, tokens, group):
+    """RotationFactor.apply-style x' = H x - (x V) W''^T on the Qwen3 widths, then
+    dynamic_asym_int4: exact projection and correction, bit-exact tuple."""
+    print(f"[test_fused_tuple_large_paley_rank] n={n} m={m} k={k} tokens={tokens}", flush=True)
+    bits = _seeded_bf16(tokens, n, 7 * n + k)
+    g = np.random.default_rng(k + n)
+    v = (g.standard_normal((n, k)) / np.sqrt(n)).astype(np.float32)
+    wt = (g.standard_normal((k, n)) * 0.05).astype(np.float32)
+    s = np.where(g.random(n) < 0.5, -1.0, 1.0).astype(np.float32)
+    res = hooks.rotate_dynamic_asym_int4(to_dev_bf16(bits), group, signs=torch.from_numpy(s).cuda(),
+                                         v=torch.from_numpy(v).cuda(), w_t=torch.from_numpy(wt).cuda())
+    torch.cuda.synchronize()
+    ref = O.quant(O.rotate(O.bf16_to_f32(bits), m, n // m, signs=s, v=v, wt=wt), group)
+    _assert_tuple_exact(_tuple_np(res), ref, f"n={n} m={m} k={k}")
+
+
 def test_large_paley_limits_raise():
     # rows beyond the 32768 channels one workgroup holds (200 x 256), and a
-    # rank term on the whole-row Paley path, are not built
+    # per-block rank term on the whole-row Paley path, are not built
     with pytest.raises(ValueError):
         hooks.full_hadamard_rows(torch.zeros((2, 51200), dtype=torch.bfloat16, device="cuda"), None)
     w_t = torch.zeros((4, 9728), dtype=torch.float32, device="cuda")
     v = torch.zeros((9728, 4), dtype=torch.float32, device="cuda")
     with pytest.raises(ValueError):
         hooks.rotate_dynamic_asym_int4(torch.zeros((2, 9728), dtype=torch.bfloat16, device="cuda"), 128,
-                                       v=v, w_t=w_t)
+                                       v=v, w_t=w_t, rank_block=128)
