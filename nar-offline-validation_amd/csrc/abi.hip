@@ -727,12 +727,14 @@ int narhip_rotate_dynamic_asym_int4(const void *x_bf16, int64_t tokens, int64_t 
         if (tokens < 0) return fail(NARHIP_EINVAL, "bad token count %lld", (long long)tokens);
         if (int rc = check_paley_rows(tokens, n, ld_x, had_m, had_q)) return rc;
         if (tokens == 0) return NARHIP_OK;
-        if (!codes || !scales_f16 || !zeros_f16 || !deq) return fail(NARHIP_EINVAL, "null tensor argument");
-        if (!aligned16(deq) || (reinterpret_cast<uintptr_t>(codes) & 7u))
-            return fail(NARHIP_EINVAL, "deq must be 16-byte aligned, codes 8-byte aligned");
+        if (!x_bf16 || !codes || !scales_f16 || !zeros_f16 || !deq) return fail(NARHIP_EINVAL, "null tensor argument");
+        if (!aligned16(x_bf16) || !aligned16(deq) || (reinterpret_cast<uintptr_t>(codes) & 7u))
+            return fail(NARHIP_EINVAL, "x and deq must be 16-byte aligned, codes 8-byte aligned");
         const size_t need = paley_tuple_bytes(tokens, n, k);
         if (!workspace || workspace_bytes < need)
             return fail(NARHIP_EWORKSPACE, "workspace of %zu bytes required, %zu given", need, workspace_bytes);
+        if (!aligned16(workspace)) return fail(NARHIP_EINVAL, "workspace must be 16-byte aligned");
+        // every argument is checked before the first launch
         float *rot = static_cast<float *>(workspace);
         float *corr = nullptr;
         if (k > 0) {
