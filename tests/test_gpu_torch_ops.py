@@ -106,6 +106,12 @@ def test_opcheck_hooks_dequantize_w4a4():
     xb = torch.randn((6, 3072), device="cuda", generator=g).to(torch.bfloat16)
     signs = torch.where(torch.arange(3072, device="cuda") % 5 == 0, -1.0, 1.0).float()
     _check(N.hadamard_rows, (xb, 12, 256, signs), "hadamard_rows 12 x 256")
+    xq = torch.randn((3, 9728), device="cuda", generator=g).to(torch.bfloat16)
+    _check(N.hadamard_rows, (xq, 76, 128, None), "hadamard_rows 76 x 128 (Paley rows)")
+    vq = torch.randn((9728, 8), device="cuda", generator=g) / 100.0
+    wq = torch.randn((8, 9728), device="cuda", generator=g) / 20.0
+    _check(N.rotate_dynamic_asym_int4, (xq, 76, 128, None, vq, wq, 9728, 128, ops.RANK_AUTO),
+           "rotate_dynamic_asym_int4 76 x 128, full-row rank 8")
     a = torch.randn((16, 512), device="cuda", generator=g).to(torch.bfloat16)
     wgt = torch.randn((24, 512), device="cuda", generator=g).to(torch.bfloat16)
     ca, sa, za = N.rotate_quant(a, 1, 128, None, None, None, None, 512, None, 128, ops.RANK_AUTO)
