@@ -21,7 +21,11 @@ template <int M, int Q, int B>
 int launch_kron_mqb(const KronArgs &a, bool quant, hipStream_t s)
 {
     const size_t lds = sizeof(float) * kron_rows<M>() * (Q + KPAD);
-    constexpr bool persist = Q >= 1024;   // 128 KB of LDS (32 padded rows): one workgroup per CU
+    // persistent (as many workgroups as are resident, each walking tokens with
+    // the next token's x requested ahead) from Q = 512 on: H28 x H512, 8192
+    // tokens, 343 -> 335 us per rotate_quant call; at Q = 256 (H12 x H256) it
+    // was slower (49.5 -> 51.7 us)
+    constexpr bool persist = Q >= 512;
     if (quant) {
         auto k = &kron_mfma_kernel<M, Q, B, true, persist>;
         if (int rc = set_lds(k, lds)) return rc;
