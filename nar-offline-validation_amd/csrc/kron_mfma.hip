@@ -46,7 +46,7 @@ __device__ __forceinline__ int fsw(int a) { return (((a >> 3) ^ (a >> 2)) & 1) <
 template <int M> constexpr int kron_rows() { return M > 16 ? 32 : M; }
 
 // PERSIST: a grid of at most one wave of workgroups walks all tokens,
-// prefetching the next token's x (pays where LDS allows one workgroup per CU);
+// prefetching the next token's x (the launcher uses it from Q = 512 on);
 // otherwise one workgroup per token.
 template <int M, int Q, int B, bool QUANT, bool PERSIST>
 __global__ void __launch_bounds__(16 * M)
