@@ -96,7 +96,7 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--config", default="downproj_8b",
                     choices=["kcache_3b", "qproj_3b", "downproj_8b", "vcache_decode_8b", "downproj_70b",
                              "e17_8b_k8", "e17_8b_k32", "e17_3b_k8", "e17_3b_k32", "e28_8b", "e28_3b",
-                             "w4a4_8b", "hook_kcache_3b", "hook_rows_8192"])
+                             "w4a4_8b", "hook_kcache_3b", "hook_rows_8192", "hook_rows_qwen3_8b"])
     ap.add_argument("--tokens", type=int, default=0,
                     help="token count of the e28_* transform settings (default 2048) and of w4a4_8b "
                          "(default 8192)")
@@ -385,7 +385,9 @@ def bench_transform_f16(args, w, dev) -> int:
 def bench_hook(args, dev) -> int:
     """The fused hook call (rotate, dynamic_asym_int4, dequantize; one kernel) through the C ABI:
     hook_kcache_3b -- the K-cache shape (2048 x 8 heads x 128 bf16, H_128 and rank 2 per head, b = 32);
-    hook_rows_8192 -- 4096 rows of 8192 bf16 (full-row FWHT, the Llama-3.2-3B down_proj width, b = 128)."""
+    hook_rows_8192 -- 4096 rows of 8192 bf16 (full-row FWHT, the Llama-3.2-3B down_proj width, b = 128);
+    hook_rows_qwen3_8b -- 2048 rows of 9728 bf16 (H_76 x H_128, the Qwen3-8B down_proj width, b = 128:
+    the whole-row Paley kernel, x' staged in a workspace, then the quantizer)."""
     import numpy as np
     import torch
 
@@ -394,6 +396,13 @@ def bench_hook(args, dev) -> int:
         w = workloads.kcache_3b(args.tokens or 2048)
         m, q, nb = 1, 128, 128
         desc = f"hook_kcache_3b: {w.tokens} x 8 heads x 128 bf16, H128 + rank 2 per head, b=32, tuple out"
+    elif args.config == "hook_rows_qwen3_8b":
+        T, n = args.tokens or 2048, 9728
+        rng = np.random.default_rng(20260902)
+        x = rng.standard_normal((T, n), dtype=np.float32)
+        w = workloads.Workload("hook_rows_qwen3_8b", workloads.bf16_bits(x), (76, 128), 128)
+        m, q, nb = 76, 128, n
+        desc = f"hook_rows_qwen3_8b: {T} x {n} bf16, H76 (Paley II) x H128 whole rows, b=128, tuple out"
     else:
         T, n = args.tokens or 4096, 8192
         rng = np.random.default_rng(20260902)
@@ -412,13 +421,15 @@ def bench_hook(args, dev) -> int:
     deq = torch.empty((T, n), dtype=torch.float32, device=dev)
     lib = _lib.load()
     ws_bytes = lib.narhip_rotate_dynamic_asym_int4_workspace(T, n, m, q, k, nb, b, 0)
-    assert ws_bytes == 0, "the fused hook shapes run in one kernel"
+    assert ws_bytes == 0 or m > 28, "the fused hook shapes run in one kernel"
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
     p = lambda t: None if t is None else ctypes.c_void_p(t.data_ptr())  # noqa: E731
     cs = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
 
     def step():
         _lib.check(lib.narhip_rotate_dynamic_asym_int4(p(x), T, n, n, m, q, None, k, nb, p(v), p(wt), b, p(codes),
-                                                       p(sc), p(zc), p(deq), 0, None, 0, cs))
+                                                       p(sc), p(zc), p(deq), 0, p(ws) if ws_bytes else None,
+                                                       ws_bytes, cs))
 
     for _ in range(args.warmup):
         step()

@@ -8,7 +8,7 @@ namespace host {
 
 int launch_paley_rows(const PaleyRowsArgs &a, hipStream_t s)
 {
-    const size_t lds = sizeof(float) * (size_t)a.m * (size_t)a.q;
+    const size_t lds = sizeof(float) * (size_t)a.m * (size_t)a.q + sizeof(uint32_t) * (size_t)a.m * paley_sign_words(a.m);
     const dim3 grid((unsigned)a.T);
     switch (a.q <= 64 ? 1 : a.q / 64) {
     case 1:
@@ -23,16 +23,8 @@ int launch_paley_rows(const PaleyRowsArgs &a, hipStream_t s)
         if (int rc = set_lds(paley_rows_kernel<4>, lds)) return rc;
         hipLaunchKernelGGL(paley_rows_kernel<4>, grid, dim3(PR_THREADS), lds, s, a);
         break;
-    case 8:
-        if (int rc = set_lds(paley_rows_kernel<8>, lds)) return rc;
-        hipLaunchKernelGGL(paley_rows_kernel<8>, grid, dim3(PR_THREADS), lds, s, a);
-        break;
-    case 16:
-        if (int rc = set_lds(paley_rows_kernel<16>, lds)) return rc;
-        hipLaunchKernelGGL(paley_rows_kernel<16>, grid, dim3(PR_THREADS), lds, s, a);
-        break;
-    default:
-        return fail(NARHIP_EUNSUPPORTED, "Paley rows need q <= 1024 (q=%d)", a.q);
+    default:   // m >= 68 and m q <= 32768 leave q <= 256
+        return fail(NARHIP_EUNSUPPORTED, "Paley rows need q <= 256 (q=%d)", a.q);
     }
     return check_launch("paley_rows_kernel");
 }

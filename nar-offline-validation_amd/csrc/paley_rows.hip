@@ -11,9 +11,10 @@
 //     fp64 before the add (the reference forms this product in fp64);
 //   other orders: |entry| = fp32(1/sqrt(m)); the product is exact in fp64 and
 //     one fma adds it.
-// The +-1 pattern is computed per term on the scalar unit from the
-// quadratic-residue table of the construction's prime (rows by waves, so the
-// row index and the term index are wave-uniform): Paley I (order p + 1, p a
+// The +-1 pattern is built once per workgroup as sign bits in LDS from the
+// quadratic-residue table of the construction's prime, and read as one word
+// per 32 terms (rows by waves, so the row and the word are wave-uniform and
+// each term's sign is a scalar bit test): Paley I (order p + 1, p a
 // prime = 3 mod 4: ones bordering Q - I, Q[r][c] = chi(r - c)) or Paley II
 // (order 2(p + 1), p = 1 mod 4: [[C + I, C - I], [C - I, -C - I]] with the
 // conference matrix C bordered by ones around Q), the constructions of
@@ -47,13 +48,14 @@ struct PaleyRowsArgs {
     uint32_t residue[8];    // bit d set <=> d is a nonzero square mod p (p < 256)
 };
 
-// Entry (r, c) of the +-1 Paley matrix is -1 (r, c < m; wave-uniform arguments).
-__device__ __forceinline__ bool paley_neg(const PaleyRowsArgs &a, int r, int c)
+// Entry (r, c) of the +-1 Paley matrix is -1 (r, c < m); res = the quadratic
+// residue bits of the construction's prime.
+__device__ __forceinline__ bool paley_neg(const PaleyRowsArgs &a, const uint32_t *res, int r, int c)
 {
     auto chi_neg = [&](int i, int j) {       // chi(i - j mod p) = -1, i != j, i, j in [1, p]
         int d = i - j;
         if (d < 0) d += a.p;
-        return ((a.residue[d >> 5] >> (d & 31)) & 1u) == 0;
+        return ((res[d >> 5] >> (d & 31)) & 1u) == 0;
     };
     if (a.kind == 1) {
         if (r == 0 || c == 0) return false;
@@ -72,14 +74,34 @@ __device__ __forceinline__ bool paley_neg(const PaleyRowsArgs &a, int r, int c)
     return v < 0;
 }
 
+// Words of sign bits per row of H_m.
+__host__ __device__ constexpr int paley_sign_words(int m) { return (m + 31) / 32; }
+
 // CPL output columns per lane (q = 64 CPL, or q < 64 with CPL = 1).
 template <int CPL>
 __global__ void __launch_bounds__(PR_THREADS)
 paley_rows_kernel(PaleyRowsArgs a)
 {
-    extern __shared__ __align__(16) float F[];          // [m][q]
+    extern __shared__ __align__(16) float F[];          // [m][q], then the sign bits [m][W]
+    __shared__ uint32_t res[8];
     const int n = a.m * a.q;
+    const int W = paley_sign_words(a.m);
+    uint32_t *sgn = reinterpret_cast<uint32_t *>(F + n);
     const int tid = threadIdx.x;
+#pragma unroll
+    for (int j = 0; j < 8; j++)
+        if (tid == j) res[j] = a.residue[j];
+    __syncthreads();
+    // the sign bits of H_m, once per workgroup: bit b of word (r, w) is entry (r, 32 w + b) < 0
+    for (int i = tid; i < a.m * W; i += PR_THREADS) {
+        const int r = i / W, w = i - r * W;
+        uint32_t bits = 0;
+        for (int b = 0; b < 32; b++) {
+            const int c = 32 * w + b;
+            if (c < a.m && paley_neg(a, res, r, c)) bits |= 1u << b;
+        }
+        sgn[i] = bits;
+    }
     const uint16_t *xr = a.x + (int64_t)blockIdx.x * a.ldx;
     for (int i = tid; i < n; i += PR_THREADS) {
         float v = __uint_as_float((uint32_t)xr[i] << 16);
@@ -110,18 +132,23 @@ paley_rows_kernel(PaleyRowsArgs a)
         double acc[CPL];
 #pragma unroll
         for (int j = 0; j < CPL; j++) acc[j] = 0.0;
-        for (int c2 = 0; c2 < a.m; c2++) {
-            const double h = paley_neg(a, ru, c2) ? -a.hm : a.hm;
-            const float *fr = F + c2 * a.q;
+        for (int w = 0; w < W; w++) {
+            const uint32_t bits = __builtin_amdgcn_readfirstlane(sgn[ru * W + w]);
+            const int cend = a.m - 32 * w < 32 ? a.m - 32 * w : 32;
+#pragma unroll 4
+            for (int b = 0; b < cend; b++) {
+                const double h = (bits >> b) & 1u ? -a.hm : a.hm;
+                const float *fr = F + (32 * w + b) * a.q;
 #pragma unroll
-            for (int j = 0; j < CPL; j++) {
-                const int c = lane + 64 * j;
-                const double f = (double)fr[c < a.q ? c : 0];
-                if (a.fp64_product) {
-                    const double pr = f * h;
-                    acc[j] = acc[j] + pr;
-                } else {
-                    acc[j] = fma(f, h, acc[j]);
+                for (int j = 0; j < CPL; j++) {
+                    const int c = lane + 64 * j;
+                    const double f = (double)fr[c < a.q ? c : 0];
+                    if (a.fp64_product) {
+                        const double pr = f * h;
+                        acc[j] = acc[j] + pr;
+                    } else {
+                        acc[j] = fma(f, h, acc[j]);
+                    }
                 }
             }
         }
