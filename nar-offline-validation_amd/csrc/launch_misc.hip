@@ -6,27 +6,34 @@
 namespace narhip {
 namespace host {
 
-int launch_paley_rows(const PaleyRowsArgs &a, hipStream_t s)
+namespace {
+
+template <int CPL, bool FP64P>
+int launch_paley_rows_t(const PaleyRowsArgs &a, size_t lds, hipStream_t s)
 {
-    const size_t lds = sizeof(float) * (size_t)a.m * (size_t)a.q + sizeof(uint32_t) * (size_t)a.m * paley_sign_words(a.m);
-    const dim3 grid((unsigned)a.T);
+    if (int rc = set_lds(paley_rows_kernel<CPL, FP64P>, lds)) return rc;
+    hipLaunchKernelGGL((paley_rows_kernel<CPL, FP64P>), dim3((unsigned)a.T), dim3(PR_THREADS), lds, s, a);
+    return check_launch("paley_rows_kernel");
+}
+
+template <bool FP64P>
+int launch_paley_rows_p(const PaleyRowsArgs &a, size_t lds, hipStream_t s)
+{
     switch (a.q <= 64 ? 1 : a.q / 64) {
-    case 1:
-        if (int rc = set_lds(paley_rows_kernel<1>, lds)) return rc;
-        hipLaunchKernelGGL(paley_rows_kernel<1>, grid, dim3(PR_THREADS), lds, s, a);
-        break;
-    case 2:
-        if (int rc = set_lds(paley_rows_kernel<2>, lds)) return rc;
-        hipLaunchKernelGGL(paley_rows_kernel<2>, grid, dim3(PR_THREADS), lds, s, a);
-        break;
-    case 4:
-        if (int rc = set_lds(paley_rows_kernel<4>, lds)) return rc;
-        hipLaunchKernelGGL(paley_rows_kernel<4>, grid, dim3(PR_THREADS), lds, s, a);
-        break;
+    case 1: return launch_paley_rows_t<1, FP64P>(a, lds, s);
+    case 2: return launch_paley_rows_t<2, FP64P>(a, lds, s);
+    case 4: return launch_paley_rows_t<4, FP64P>(a, lds, s);
     default:   // m >= 68 and m q <= 32768 leave q <= 256
         return fail(NARHIP_EUNSUPPORTED, "Paley rows need q <= 256 (q=%d)", a.q);
     }
-    return check_launch("paley_rows_kernel");
+}
+
+}  // namespace
+
+int launch_paley_rows(const PaleyRowsArgs &a, hipStream_t s)
+{
+    const size_t lds = sizeof(float) * (size_t)a.m * (size_t)a.q + sizeof(uint32_t) * (size_t)a.m * paley_sign_words(a.m);
+    return a.fp64_product ? launch_paley_rows_p<true>(a, lds, s) : launch_paley_rows_p<false>(a, lds, s);
 }
 
 int launch_dequant(const uint8_t *codes, const uint16_t *scales, const uint16_t *zeros, int64_t rows, int64_t n,

@@ -77,8 +77,10 @@ __device__ __forceinline__ bool paley_neg(const PaleyRowsArgs &a, const uint32_t
 // Words of sign bits per row of H_m.
 __host__ __device__ constexpr int paley_sign_words(int m) { return (m + 31) / 32; }
 
-// CPL output columns per lane (q = 64 CPL, or q < 64 with CPL = 1).
-template <int CPL>
+// CPL output columns per lane (q = 64 CPL, or q < 64 with CPL = 1); FP64P:
+// products rounded in fp64 (a.fp64_product), as a template argument so that
+// the term loop has no branch.
+template <int CPL, bool FP64P>
 __global__ void __launch_bounds__(PR_THREADS)
 paley_rows_kernel(PaleyRowsArgs a)
 {
@@ -143,7 +145,7 @@ paley_rows_kernel(PaleyRowsArgs a)
                 for (int j = 0; j < CPL; j++) {
                     const int c = lane + 64 * j;
                     const double f = (double)fr[c < a.q ? c : 0];
-                    if (a.fp64_product) {
+                    if constexpr (FP64P) {
                         const double pr = f * h;
                         acc[j] = acc[j] + pr;
                     } else {
